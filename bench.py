@@ -1,0 +1,287 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path: one call of ``program.run`` = one step.
+
+Default workload: C5, the long-tail bf16 D=128 segmented softmax (8,192
+segments, 4,194,304 rows, longest 200,000, i64 offsets, max_len passed) on
+one MI355X, inputs resident in HBM. Prints ONE JSON line:
+
+* ``value``: achieved GB/s of algorithmic bytes (read values + offsets once,
+  write the output once) per call; ``us_per_call`` and ``pct_of_peak`` beside it.
+* ``roofline``: the dominant kernel's algorithmic bytes / its average
+  duration (HIP events recorded around every launch inside the timed calls,
+  on the stream the kernels run on), against the 8 TB/s HBM peak.
+* ``cpu_baseline``: the float64 NumPy oracle timed on this host on a bounded
+  sample of the same workload, scaled to µs per full call.
+
+Every measured configuration first passes the oracle (max bit-exact,
+sum/softmax within tolerance) on a sample of its segments.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--cold] [--all]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+from pathlib import Path
+import sys
+import tempfile
+import time
+
+ROOT = Path(__file__).resolve().parent
+for _path in (ROOT, ROOT / "ragged-mlir_amd"):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+import numpy as np  # noqa: E402
+
+PEAK_GBPS = 8000.0
+METRIC = "µs/call + achieved HBM GB/s (% of peak), long-tail bf16 D=128 softmax"
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def sample_segments(lengths: np.ndarray, count: int, seed: int) -> np.ndarray:
+    """Segment ids for the oracle gate: the longest, the shortest, empties and
+    a random spread."""
+    rng = np.random.default_rng(seed)
+    b = len(lengths)
+    picks = {int(np.argmax(lengths)), int(np.argmin(lengths)), 0, b - 1}
+    picks.update(int(i) for i in rng.choice(b, size=min(b, count), replace=False))
+    return np.array(sorted(picks), dtype=np.int64)
+
+
+def gather_segments(values, offsets, ids):
+    """Rows of the chosen segments, packed, with their own offsets."""
+    lo, hi = offsets[ids].astype(np.int64), offsets[ids + 1].astype(np.int64)
+    rows = np.concatenate([np.arange(a, b) for a, b in zip(lo, hi)]) if len(ids) else np.zeros(0, np.int64)
+    sub_offsets = np.concatenate([[0], np.cumsum(hi - lo)]).astype(np.int64)
+    return rows, sub_offsets
+
+
+def oracle_gate(op, dtype, values_f32, offsets, out_device, torch, *, max_rows=600_000, seed=0):
+    """Check a sample of segments (independent of each other) against the
+    float64 oracle. Returns the oracle's error statistics."""
+    import oracle
+    lengths = np.diff(offsets.astype(np.int64))
+    ids = sample_segments(lengths, 64, seed)
+    # Keep the sample bounded: drop the largest picks until it fits.
+    while lengths[ids].sum() > max_rows and len(ids) > 1:
+        ids = np.delete(ids, int(np.argmax(lengths[ids])))
+    rows, sub_offsets = gather_segments(values_f32, offsets, ids)
+    inputs = values_f32[rows]
+    if dtype == "bf16":
+        inputs = oracle.quantize_bf16(inputs)
+    if op == "softmax":
+        actual = out_device[torch.from_numpy(rows).to(out_device.device)].float().cpu().numpy()
+    else:
+        actual = out_device[torch.from_numpy(ids).to(out_device.device)].float().cpu().numpy()
+    stats = oracle.assert_matches(actual.astype(np.float64), inputs, sub_offsets, operation=op, input_dtype=dtype)
+    if op == "max":
+        expected = oracle.segment_max(inputs, sub_offsets).astype(np.float32)
+        if dtype == "bf16":
+            expected = oracle.quantize_bf16(expected)
+        nan = np.isnan(expected)
+        assert np.array_equal(nan, np.isnan(actual)) and np.array_equal(actual[~nan], expected[~nan])
+    stats["segments_checked"] = int(len(ids))
+    stats["rows_checked"] = int(len(rows))
+    return stats
+
+
+def cpu_baseline(op, dtype, values_f32, offsets, *, target_seconds=8.0):
+    """Time the NumPy oracle (single thread) on a prefix of segments that holds
+    about 1/16 of the rows, scaled to µs per full call."""
+    import oracle
+    lengths = np.diff(offsets.astype(np.int64))
+    n = int(offsets[-1])
+    cut = int(np.searchsorted(np.cumsum(lengths), max(1, n // 16))) + 1
+    cut = min(cut, len(lengths))
+    sample_offsets = offsets[:cut + 1].astype(np.int64)
+    rows = int(sample_offsets[-1])
+    inputs = values_f32[:rows]
+    if dtype == "bf16":
+        inputs = oracle.quantize_bf16(inputs)
+    function = {"sum": oracle.segment_sum, "max": oracle.segment_max, "softmax": oracle.segment_softmax}[op]
+    function(inputs, sample_offsets)   # warm-up
+    times, started = [], time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - started) < target_seconds or len(times) < 1:
+        t0 = time.perf_counter()
+        function(inputs, sample_offsets)
+        times.append(time.perf_counter() - t0)
+    per_call_us = float(np.median(times)) * 1e6 * (n / max(rows, 1))
+    return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": 1, "kind": "port",
+            "sample": f"float64 NumPy oracle ({op}) on the first {cut} of {len(lengths)} segments "
+                      f"({rows} of {n} rows), median of {len(times)} runs, scaled by N/rows"}
+
+
+def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_wave: int, t_block: int) -> int:
+    """Algorithmic bytes of the rows one kernel role owns."""
+    if role == "naive":
+        rows = lengths
+    elif role == "wave":
+        rows = lengths[lengths <= t_wave]
+    elif role == "block":
+        rows = lengths[(lengths > t_wave) & (lengths <= t_block)]
+    elif role in ("split_partial", "split_normalize", "split_combine"):
+        rows = lengths[lengths > t_block]
+    else:
+        return 0
+    n_rows, segs = int(rows.sum()), int(len(rows))
+    if op == "softmax":
+        if role == "split_partial":
+            return n_rows * d * element          # reads the rows once
+        if role == "split_normalize":
+            return n_rows * d * element          # writes the rows once (its re-read is not algorithmic)
+        if role == "split_combine":
+            return 0
+        return 2 * n_rows * d * element
+    if role == "split_combine":
+        return segs * d * element                # writes the outputs
+    return n_rows * d * element + (0 if role == "split_partial" else segs * d * element)
+
+
+def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
+    from ragged import Compiler, ProgramSpec
+    from ragged.workloads import CONFIGS, algorithmic_bytes
+    from ragged.runtime import _modules
+
+    t0 = time.perf_counter()
+    workload = CONFIGS[name](seed)
+    log(f"[bench] {workload.name}: N={workload.n} B={workload.b} D={workload.d} generated in "
+        f"{time.perf_counter() - t0:.1f}s")
+    device = torch.device("cuda", 0)
+    tdtype = torch.bfloat16 if workload.dtype == "bf16" else torch.float32
+    element = 2 if workload.dtype == "bf16" else 4
+    offset_bytes = 4 if workload.offsets_dtype == "i32" else 8
+    x = torch.from_numpy(workload.values).to(device).to(tdtype).contiguous()
+    off = torch.from_numpy(workload.offsets).to(device)
+    lengths = np.diff(workload.offsets.astype(np.int64))
+    max_len = workload.max_len if workload.pass_max_len else None
+    results = []
+    for op in workload.ops:
+        program = Compiler().compile(ProgramSpec(op, workload.dtype, workload.d, workload.offsets_dtype), cache)
+        rows = workload.n if op == "softmax" else workload.b
+        out = torch.empty((rows, workload.d), dtype=tdtype, device=device)
+        selects = ["auto", "classified", "naive"] if args.all else ["auto"]
+        for select in selects:
+            report = program.run(x, off, out, select=select, max_len=max_len)
+            torch.cuda.synchronize()
+            stats = oracle_gate(op, workload.dtype, workload.values, workload.offsets, out, torch, seed=seed)
+            log(f"[bench] {workload.name} {op} {select} ({report.selected}): oracle ok, "
+                f"max_fraction_of_tolerance={stats['max_fraction_of_tolerance']:.3g} on "
+                f"{stats['segments_checked']} segments")
+            for _ in range(args.warmup):
+                program.run(x, off, out, select=select, max_len=max_len)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            flush = torch.empty((1 << 30,), dtype=torch.uint8, device=device) if args.cold else None
+            if args.cold:
+                total_ms = 0.0
+                for _ in range(args.steps):
+                    flush.fill_(1)
+                    start.record()
+                    program.run(x, off, out, select=select, max_len=max_len)
+                    end.record()
+                    torch.cuda.synchronize()
+                    total_ms += start.elapsed_time(end)
+                ms = total_ms / args.steps
+            else:
+                torch.cuda.synchronize()
+                start.record()
+                for _ in range(args.steps):
+                    program.run(x, off, out, select=select, max_len=max_len)
+                end.record()
+                torch.cuda.synchronize()
+                ms = start.elapsed_time(end) / args.steps
+            # Per-kernel durations: events around every launch of K more calls.
+            chosen = program.naive if report.selected == "naive" else program
+            module = _modules[(0, chosen._digest)]
+            module.profile_start(args.steps)
+            for _ in range(args.steps):
+                if args.cold:
+                    flush.fill_(1)
+                program.run(x, off, out, select=select, max_len=max_len)
+            profile = module.profile_stop()
+            torch.cuda.synchronize()
+            plan = chosen._plans[(0, workload.n, workload.b)]
+            total_bytes = algorithmic_bytes(op, workload.n, workload.b, workload.d, element, offset_bytes)
+            kernels = {}
+            for role, entry in profile["roles"].items():
+                avg = entry["ms"] / max(entry["launches"], 1)
+                nbytes = role_bytes(role, op, lengths, workload.d, element, int(plan.t_wave), int(plan.t_block))
+                kernels[role] = {"avg_ms": round(avg, 5), "bytes": nbytes,
+                                 "gbps": round(nbytes / (avg * 1e-3) / 1e9, 1) if avg > 0 else None}
+            dominant = max(kernels, key=lambda r: kernels[r]["avg_ms"]) if kernels else None
+            gpu_ms = profile["call_ms"] / max(profile["calls"], 1)
+            gbps = total_bytes / (ms * 1e-3) / 1e9
+            results.append({
+                "workload": workload.name, "op": op, "select": select, "selected": report.selected,
+                "us_per_call": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
+                "gpu_us_per_call": round(gpu_ms * 1e3, 2), "algorithmic_bytes": total_bytes, "kernels": kernels,
+                "dominant": dominant, "cold": bool(args.cold), "oracle": stats,
+                "n": workload.n, "b": workload.b, "d": workload.d, "dtype": workload.dtype,
+                "offsets_dtype": workload.offsets_dtype, "max_len": workload.max_len,
+                "kernel_names": list(report.kernel_names), "grids": [list(g) for g in report.grids]})
+            log(f"[bench] {workload.name} {op} {select}: {ms * 1e3:.1f} us/call, {gbps:.0f} GB/s "
+                f"({100 * gbps / PEAK_GBPS:.1f}% of peak); kernels {json.dumps(kernels)}")
+    return results, workload
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
+    parser.add_argument("--cold", action="store_true", help="flush 1 GiB (> MALL + L2) before every call")
+    parser.add_argument("--all", action="store_true", help="also measure forced classified and naive schedules")
+    parser.add_argument("--details", type=Path, help="write every measured record as JSON to this file")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = parser.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+    from ragged import ArtifactCache
+    with tempfile.TemporaryDirectory(prefix="ragged-bench-") as directory:
+        cache = ArtifactCache(directory)
+        records, workload = run_config(args.config, args, torch, cache)
+        headline = next(r for r in records if r["select"] == "auto")
+        baseline = None
+        if not args.no_cpu:
+            baseline = cpu_baseline(headline["op"], workload.dtype, workload.values, workload.offsets)
+            baseline["cores"] = 1
+            log(f"[bench] cpu baseline: {baseline}")
+    dominant = headline["dominant"]
+    kernel = headline["kernels"].get(dominant, {})
+    roofline = {"bound": "hbm", "kernel": dominant, "achieved": kernel.get("gbps"), "peak": PEAK_GBPS,
+                "unit": "GB/s", "frac": round(kernel["gbps"] / PEAK_GBPS, 4) if kernel.get("gbps") else None,
+                "traffic": None, "avg_ms": kernel.get("avg_ms"), "bytes_per_launch": kernel.get("bytes"),
+                "call_gbps_gpu_time": round(headline["algorithmic_bytes"] / (headline["gpu_us_per_call"] * 1e-6) / 1e9, 1)}
+    line = {
+        "metric": METRIC, "value": headline["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(headline["us_per_call"] / 1e3, 5),
+        "us_per_call": headline["us_per_call"], "pct_of_peak": headline["pct_of_peak"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": headline["dtype"], "data": "synthetic (seeded NumPy generators, resident in HBM)",
+        "config": {"workload": headline["workload"], "op": headline["op"], "n": headline["n"], "b": headline["b"],
+                   "d": headline["d"], "offsets": headline["offsets_dtype"], "max_len": headline["max_len"],
+                   "schedule": headline["selected"], "cache": "cold" if args.cold else "warm",
+                   "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": baseline,
+    }
+    if args.details:
+        args.details.parent.mkdir(parents=True, exist_ok=True)
+        args.details.write_text(json.dumps({"line": line, "records": records}, indent=1) + "\n")
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,184 @@
+/* C ABI of libragged_hip.so: segmented sum / max / softmax on gfx950.
+ *
+ * This library replaces the reference's native launcher
+ * (simon-jd/ragged-mlir runtime/Driver.h:21-54 and runtime/bindings.cpp:11-37,
+ * the nanobind module ragged._native.DriverModule) together with the kernels
+ * the reference generated through MLIR -> NVVM -> PTX
+ * (lib/Conversion/ToGPU.cpp). The kernels are hand-written HIP compiled ahead
+ * of time for gfx950, so there is no module loading from a code blob: a
+ * "module" is a handle on one kernel specialisation (op, dtype, offsets
+ * dtype, feature width, mask) on one device.
+ *
+ * Conventions
+ *  - Every function returns RG_OK (0) or a negative RG_E_* status; the
+ *    calling thread's message is then available from rg_last_error().
+ *  - No function allocates device memory. The caller owns values, offsets,
+ *    out, mask and the workspace, and passes raw device pointers.
+ *  - rg_run and rg_check_offsets only enqueue work on the given HIP stream;
+ *    they never synchronise. On error nothing has been launched.
+ *  - All handles are thread-compatible: concurrent calls on one module are
+ *    safe (it is immutable after creation).
+ */
+#ifndef RAGGED_HIP_H
+#define RAGGED_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RG_ABI_VERSION 1
+
+enum rg_status {
+  RG_OK = 0,
+  RG_E_INVALID = -1,      /* bad argument or specialisation */
+  RG_E_DEVICE = -2,       /* HIP runtime error (device, launch, occupancy) */
+  RG_E_UNSUPPORTED = -3,  /* device is not gfx950 */
+  RG_E_WORKSPACE = -4     /* workspace missing or too small for the plan */
+};
+
+enum rg_op { RG_OP_SUM = 0, RG_OP_MAX = 1, RG_OP_SOFTMAX = 2 };
+enum rg_dtype { RG_F32 = 0, RG_BF16 = 1 };
+enum rg_index { RG_I32 = 0, RG_I64 = 1 };
+enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1 };
+
+/* Kernel roles, in launch order of the classified schedule. */
+enum rg_role {
+  RG_ROLE_INIT = 0,
+  RG_ROLE_CLASSIFY = 1,
+  RG_ROLE_WAVE = 2,            /* wave64 worker: one wave per short segment */
+  RG_ROLE_BLOCK = 3,           /* workgroup worker: one 256-thread group per segment */
+  RG_ROLE_SPLIT_PARTIAL = 4,   /* one workgroup per part of a long segment */
+  RG_ROLE_SPLIT_COMBINE = 5,   /* fold the parts of each long segment */
+  RG_ROLE_SPLIT_NORMALIZE = 6, /* softmax: normalise each part */
+  RG_ROLE_NAIVE = 7,           /* block-per-segment schedule */
+  RG_ROLE_COUNT = 8
+};
+
+#define RG_MAX_LAUNCHES 8
+#define RG_WORKSPACE_BUFFERS 9
+
+/* A kernel specialisation (ProgramSpec fields that change device code;
+ * reference: python/ragged/model.py:129-188). */
+typedef struct rg_spec {
+  int32_t op;             /* rg_op */
+  int32_t dtype;          /* rg_dtype: values and out */
+  int32_t offsets_dtype;  /* rg_index */
+  int32_t feature_dim;    /* D in [1, 1024] */
+  float scale;            /* f32 multiplier of every input (1 = none) */
+  int32_t has_mask;       /* softmax only: additive f32 [N, D] mask */
+  int32_t vectorize;      /* 0: one element per access (any alignment) */
+  int32_t debug_visits;   /* classified only: count final writes per segment */
+  int64_t t_wave;         /* wave class: segments of at most t_wave rows; <0: default */
+  int64_t t_block;        /* block class: at most t_block rows; <0: default */
+  int64_t part_rows;      /* rows per split part; <0: default */
+} rg_spec;
+
+/* Device facts the host cost model and grids use. */
+typedef struct rg_device_props {
+  int32_t ordinal;
+  int32_t cu_count;          /* compute units */
+  int32_t xcd_count;         /* accelerator complex dies (own L2 each) */
+  int32_t wave_size;
+  int64_t l2_bytes;          /* L2 per XCD as reported by the runtime */
+  int64_t mall_bytes;        /* last-level (Infinity) cache; 0 if unknown */
+  int64_t lds_per_cu;
+  int64_t global_mem_bytes;
+  char arch[64];             /* gcnArchName, e.g. "gfx950:sramecc+:xnack-" */
+} rg_device_props;
+
+/* Resolved launch sequence and workspace layout for one (N, B, schedule)
+ * (reference: runtime.py:145-162 scratch layout, layout.py:50-107). */
+typedef struct rg_plan {
+  int32_t schedule;                       /* rg_schedule */
+  int32_t launches;                       /* kernels in submission order */
+  int32_t roles[RG_MAX_LAUNCHES];         /* rg_role of each launch */
+  uint32_t grid[RG_MAX_LAUNCHES][3];
+  uint32_t block[RG_MAX_LAUNCHES];
+  uint32_t lds_bytes[RG_MAX_LAUNCHES];    /* static LDS of each kernel */
+  uint64_t workspace_bytes;               /* one allocation, buffers 256-B aligned */
+  uint64_t buffer_offset[RG_WORKSPACE_BUFFERS];
+  uint64_t buffer_bytes[RG_WORKSPACE_BUFFERS];
+  int64_t n, b;
+  int64_t b_split;                        /* rows of the split statistics */
+  int64_t items_cap;                      /* capacity of the split item table */
+  int64_t t_wave, t_block, part_rows;
+  int32_t vec;                            /* elements per vector access */
+  int32_t flat;                           /* 1: flat mapping (D < vec) */
+} rg_plan;
+
+/* Workspace buffer indices (rg_plan.buffer_offset / buffer_bytes). */
+enum rg_buffer {
+  RG_BUF_COUNTERS = 0,      /* i64[4] class counts and split items */
+  RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class */
+  RG_BUF_ITEM_POS = 2,      /* i64[items_cap] split position of each item */
+  RG_BUF_PART_BEGIN = 3,    /* i64[B_split] first item of each split segment */
+  RG_BUF_PARTIALS = 4,      /* f32[items_cap, D] */
+  RG_BUF_PARTIAL_SUMS = 5,  /* f32[items_cap, D] (softmax) */
+  RG_BUF_STATS_MAX = 6,     /* f32[B_split, D] (softmax) */
+  RG_BUF_STATS_SUM = 7,     /* f32[B_split, D] (softmax) */
+  RG_BUF_VISITS = 8         /* i32[B] (debug_visits) */
+};
+
+typedef struct rg_module rg_module;
+
+/* ABI version of the library (RG_ABI_VERSION). */
+int rg_abi_version(void);
+
+/* Identity of the build: target, flags and source digest. */
+const char* rg_build_info(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* rg_last_error(void);
+
+/* Device facts; replaces the occupancy/L2 queries of runtime.py:165-178. */
+int rg_device_query(int ordinal, rg_device_props* out);
+
+/* Fill the default class thresholds and part size of `spec` (fields < 0). */
+int rg_spec_defaults(rg_spec* spec);
+
+/* Create a kernel specialisation on a device; replaces
+ * DriverModule(cubin, target) (Driver.h:23-27, Driver.cpp:178-195). Fails with
+ * RG_E_UNSUPPORTED unless the device is gfx950. */
+int rg_module_create(int device, const rg_spec* spec, rg_module** out);
+
+/* Release a module; replaces DriverModule.close() (Driver.h:44). Work already
+ * enqueued is unaffected (kernels are not unloaded). */
+void rg_module_destroy(rg_module* module);
+
+/* Resident workgroups of one role on the whole device (one resident wave
+ * of the persistent workers); replaces resident_blocks (Driver.cpp:236-245). */
+int rg_module_resident(const rg_module* module, int role, int64_t* blocks);
+
+/* Resolve launches and workspace for N rows, B segments; replaces
+ * add_plan (Driver.cpp:272-292). Pure host arithmetic, overflow checked. */
+int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, rg_plan* plan);
+
+/* Enqueue the plan on `stream` (a hipStream_t); replaces run_plan
+ * (Driver.cpp:299-353). `workspace` must hold plan->workspace_bytes bytes
+ * (may be NULL when that is 0); `mask` is NULL unless the module has one. */
+int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
+           void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* Measurement: while profiling is on, rg_run records a HIP event before
+ * every launch and after the last one (no synchronisation), for at most
+ * `max_calls` calls. rg_profile_stop waits for those events and returns, per
+ * role, the summed kernel milliseconds and launch counts, and the summed
+ * whole-call milliseconds. Not thread-safe; measurement only. */
+int rg_profile_start(rg_module* module, int max_calls);
+int rg_profile_stop(rg_module* module, double* role_ms, int64_t* role_launches, double* call_ms,
+                    int64_t* calls);
+
+/* Checked mode: write into status[7] (device i64) the earliest offending
+ * index of each offsets condition, INT64_MAX if none (docs/checked-abi.md;
+ * replaces the offsets_init / offsets_check kernels, ToGPU.cpp:1067-1189).
+ * min_len / max_len < 0 mean "no hint". Enqueue only. */
+int rg_check_offsets(int device, int offsets_dtype, const void* offsets, int64_t n, int64_t b,
+                     int64_t min_len, int64_t max_len, int64_t* status, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RAGGED_HIP_H */

@@ -1,0 +1,501 @@
+// Host implementation of the C ABI in include/ragged_hip.h.
+//
+// Replaces the reference's CUDA Driver API launcher (runtime/Driver.cpp):
+// instead of loading a generated cubin and resolving kernels by name, a
+// module selects one of the ahead-of-time compiled gfx950 kernel
+// specialisations; instead of a launch plan with relocated memref
+// descriptors, one by-value Params struct carries every pointer and size.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/ragged_hip.h"
+#include "device.hpp"
+#include "table.hpp"
+
+#ifndef RG_SOURCE_DIGEST
+#define RG_SOURCE_DIGEST "unknown"
+#endif
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int status, const char* fmt, ...) {
+  char buffer[512];
+  va_list args;
+  va_start(args, fmt);
+  vsnprintf(buffer, sizeof buffer, fmt, args);
+  va_end(args);
+  g_error = buffer;
+  return status;
+}
+
+int hip_fail(hipError_t err, const char* what) {
+  return fail(RG_E_DEVICE, "%s: %s (%d): %s", what, hipGetErrorName(err), (int)err, hipGetErrorString(err));
+}
+
+constexpr int64_t kI64Max = INT64_MAX;
+constexpr uint64_t kAlign = 256;
+constexpr int64_t kGridMax = 2147483647;
+
+// Class boundaries and part size in bytes of segment data; row thresholds
+// follow from the row size (see rg_spec_defaults).
+constexpr int64_t kWaveBytes = 8 << 10;     // one wave64 reads up to 8 KiB
+constexpr int64_t kBlockBytes = 128 << 10;  // one workgroup reads up to 128 KiB
+constexpr int64_t kPartBytes = 64 << 10;    // a split part is 64 KiB of rows
+
+int element_bytes(int dtype) { return dtype == RG_BF16 ? 2 : 4; }
+
+// Geometry of a specialisation: elements per access and mapping, plus the
+// table index (see table.hpp).
+struct Geometry {
+  int vec;
+  bool flat;
+  int index;
+};
+
+Geometry choose_geometry(int dtype, int d, bool vectorize) {
+  const int widest = 16 / element_bytes(dtype);   // 4 f32 or 8 bf16 per 16 B
+  if (!vectorize) return {1, false, 0};
+  if (d < widest && widest % d == 0) return {widest, true, dtype == RG_BF16 ? 4 : 3};
+  int vec = 1;
+  while (vec * 2 <= widest && d % (vec * 2) == 0) vec *= 2;
+  int index = vec == 1 ? 0 : vec == 2 ? 1 : vec == 4 ? 2 : 3;
+  return {vec, false, index};
+}
+
+int next_pow2_capped(int64_t value, int cap) {
+  int p = 1;
+  while (p < value && p < cap) p <<= 1;
+  return p;
+}
+
+// Feature tiles of a ROW launch with groups of `g` threads.
+int64_t feature_tiles(int d, int vec, bool flat, int g) {
+  if (flat) return 1;
+  const int64_t lanes = (d + vec - 1) / vec;
+  const int lpr = next_pow2_capped(lanes, g);
+  return (lanes + lpr - 1) / lpr;
+}
+
+int combine_features_host(int d) { return next_pow2_capped(d, rg::kCombineFeatures); }
+
+bool mul_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_mul_overflow(a, b, out) && *out >= 0; }
+bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow(a, b, out) && *out >= 0; }
+
+}  // namespace
+
+// Event pool of a profiling session: launches+1 events per recorded call.
+struct Profile {
+  bool active = false;
+  int max_calls = 0;
+  std::vector<hipEvent_t> events;
+  std::vector<int> call_first;     // first event index of each call
+  std::vector<int> call_roles;     // roles of every launch, concatenated
+  std::vector<int> call_launches;  // launches of each call
+};
+
+struct rg_module {
+  int device;
+  rg_spec spec;
+  Geometry geometry;
+  const rg::KernelSet* kernels;
+  const void* roles[RG_ROLE_COUNT];
+  int64_t resident[RG_ROLE_COUNT];
+  uint32_t lds[RG_ROLE_COUNT];
+  mutable Profile profile;
+};
+
+extern "C" {
+
+int rg_abi_version(void) { return RG_ABI_VERSION; }
+
+const char* rg_build_info(void) {
+  return "target=gfx950;abi=" "1" ";flags=-O3 -packed-fp32-ops;source=" RG_SOURCE_DIGEST;
+}
+
+const char* rg_last_error(void) { return g_error.c_str(); }
+
+int rg_device_query(int ordinal, rg_device_props* out) {
+  if (!out) return fail(RG_E_INVALID, "rg_device_query: null output");
+  hipDeviceProp_t prop;
+  hipError_t err = hipGetDeviceProperties(&prop, ordinal);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDeviceProperties");
+  std::memset(out, 0, sizeof *out);
+  out->ordinal = ordinal;
+  out->cu_count = prop.multiProcessorCount;
+  int xcc = 0;
+  if (hipDeviceGetAttribute(&xcc, hipDeviceAttributeNumberOfXccs, ordinal) != hipSuccess || xcc <= 0) xcc = 1;
+  out->xcd_count = xcc;
+  out->wave_size = prop.warpSize;
+  out->l2_bytes = prop.l2CacheSize;
+  // HIP reports no last-level cache size; MI350-series (gfx950) carries a
+  // 256 MiB Infinity Cache.
+  out->mall_bytes = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? (int64_t)256 << 20 : 0;
+  out->lds_per_cu = prop.maxSharedMemoryPerMultiProcessor;
+  out->global_mem_bytes = (int64_t)prop.totalGlobalMem;
+  std::snprintf(out->arch, sizeof out->arch, "%s", prop.gcnArchName);
+  return RG_OK;
+}
+
+int rg_spec_defaults(rg_spec* spec) {
+  if (!spec) return fail(RG_E_INVALID, "rg_spec_defaults: null spec");
+  if (spec->feature_dim < 1 || spec->feature_dim > 1024) return fail(RG_E_INVALID, "feature_dim must be in [1, 1024]");
+  if (spec->dtype != RG_F32 && spec->dtype != RG_BF16) return fail(RG_E_INVALID, "dtype must be f32 or bf16");
+  const int64_t row = (int64_t)spec->feature_dim * element_bytes(spec->dtype);
+  if (spec->t_wave < 0) spec->t_wave = std::max<int64_t>(1, kWaveBytes / row);
+  if (spec->t_block < 0) spec->t_block = std::max<int64_t>(spec->t_wave + 1, kBlockBytes / row);
+  if (spec->part_rows < 0) spec->part_rows = std::max<int64_t>(1, kPartBytes / row);
+  return RG_OK;
+}
+
+int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
+  if (!spec_in || !out) return fail(RG_E_INVALID, "rg_module_create: null argument");
+  *out = nullptr;
+  rg_spec spec = *spec_in;
+  if (spec.op < RG_OP_SUM || spec.op > RG_OP_SOFTMAX) return fail(RG_E_INVALID, "op must be sum, max or softmax");
+  if (spec.offsets_dtype != RG_I32 && spec.offsets_dtype != RG_I64)
+    return fail(RG_E_INVALID, "offsets dtype must be i32 or i64");
+  int status = rg_spec_defaults(&spec);
+  if (status) return status;
+  if (spec.has_mask && spec.op != RG_OP_SOFTMAX) return fail(RG_E_INVALID, "an additive mask is only defined for softmax");
+  if (!(spec.scale == spec.scale) || spec.scale > 3.402823466e38f || spec.scale < -3.402823466e38f)
+    return fail(RG_E_INVALID, "scale must be a finite f32");
+  if (spec.t_wave < 0 || spec.t_block <= spec.t_wave || spec.part_rows < 1)
+    return fail(RG_E_INVALID, "thresholds must satisfy 0 <= t_wave < t_block and part_rows >= 1");
+
+  hipDeviceProp_t prop;
+  hipError_t err = hipGetDeviceProperties(&prop, device);
+  if (err != hipSuccess) return hip_fail(err, "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(RG_E_UNSUPPORTED, "device %d is %s; this library holds gfx950 code only", device, prop.gcnArchName);
+
+  rg_module* module = new (std::nothrow) rg_module();
+  if (!module) return fail(RG_E_INVALID, "out of host memory");
+  module->device = device;
+  module->spec = spec;
+  module->geometry = choose_geometry(spec.dtype, spec.feature_dim, spec.vectorize != 0);
+  const int g = module->geometry.index;
+  if (spec.op == RG_OP_SUM) module->kernels = rg::kernels_sum(spec.dtype, spec.offsets_dtype, g);
+  else if (spec.op == RG_OP_MAX) module->kernels = rg::kernels_max(spec.dtype, spec.offsets_dtype, g);
+  else module->kernels = rg::kernels_softmax(spec.dtype, spec.offsets_dtype, g, spec.has_mask != 0);
+  const rg::KernelSet& k = *module->kernels;
+  if (!k.naive || k.vec != module->geometry.vec || k.flat != module->geometry.flat) {
+    delete module;
+    return fail(RG_E_INVALID, "no compiled kernel for this dtype/feature geometry");
+  }
+  module->roles[RG_ROLE_INIT] = rg::kernel_init();
+  module->roles[RG_ROLE_CLASSIFY] = rg::kernel_classify(spec.offsets_dtype);
+  module->roles[RG_ROLE_WAVE] = k.wave;
+  module->roles[RG_ROLE_BLOCK] = k.block;
+  module->roles[RG_ROLE_SPLIT_PARTIAL] = k.split_partial;
+  module->roles[RG_ROLE_SPLIT_COMBINE] = k.split_combine;
+  module->roles[RG_ROLE_SPLIT_NORMALIZE] = k.split_normalize;
+  module->roles[RG_ROLE_NAIVE] = k.naive;
+
+  int previous = 0;
+  err = hipGetDevice(&previous);
+  if (err == hipSuccess) err = hipSetDevice(device);
+  if (err != hipSuccess) {
+    delete module;
+    return hip_fail(err, "hipSetDevice");
+  }
+  for (int role = 0; role < RG_ROLE_COUNT; ++role) {
+    module->resident[role] = 0;
+    module->lds[role] = 0;
+    if (!module->roles[role]) continue;
+    hipFuncAttributes attributes;
+    err = hipFuncGetAttributes(&attributes, module->roles[role]);
+    if (err != hipSuccess) break;
+    module->lds[role] = (uint32_t)attributes.sharedSizeBytes;
+    int per_cu = 0;
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, module->roles[role], rg::kBlock, 0);
+    if (err != hipSuccess) break;
+    module->resident[role] = (int64_t)std::max(per_cu, 1) * prop.multiProcessorCount;
+  }
+  (void)hipSetDevice(previous);
+  if (err != hipSuccess) {
+    delete module;
+    return hip_fail(err, "kernel occupancy query");
+  }
+  *out = module;
+  return RG_OK;
+}
+
+static void release_events(Profile& profile) {
+  for (hipEvent_t event : profile.events) (void)hipEventDestroy(event);
+  profile.events.clear();
+  profile.call_first.clear();
+  profile.call_roles.clear();
+  profile.call_launches.clear();
+}
+
+void rg_module_destroy(rg_module* module) {
+  if (module) release_events(module->profile);
+  delete module;
+}
+
+int rg_profile_start(rg_module* module, int max_calls) {
+  if (!module || max_calls < 1 || max_calls > 100000) return fail(RG_E_INVALID, "rg_profile_start: bad argument");
+  Profile& profile = module->profile;
+  release_events(profile);
+  profile.active = true;
+  profile.max_calls = max_calls;
+  return RG_OK;
+}
+
+int rg_profile_stop(rg_module* module, double* role_ms, int64_t* role_launches, double* call_ms, int64_t* calls) {
+  if (!module || !role_ms || !role_launches || !call_ms || !calls) return fail(RG_E_INVALID, "rg_profile_stop: null");
+  Profile& profile = module->profile;
+  profile.active = false;
+  for (int r = 0; r < RG_ROLE_COUNT; ++r) {
+    role_ms[r] = 0;
+    role_launches[r] = 0;
+  }
+  *call_ms = 0;
+  *calls = (int64_t)profile.call_first.size();
+  hipError_t err = hipSuccess;
+  if (!profile.events.empty()) err = hipEventSynchronize(profile.events.back());
+  size_t role_index = 0;
+  for (size_t c = 0; c < profile.call_first.size() && err == hipSuccess; ++c) {
+    const int first = profile.call_first[c], launches = profile.call_launches[c];
+    for (int i = 0; i < launches && err == hipSuccess; ++i) {
+      float ms = 0;
+      err = hipEventElapsedTime(&ms, profile.events[first + i], profile.events[first + i + 1]);
+      const int role = profile.call_roles[role_index++];
+      role_ms[role] += ms;
+      role_launches[role] += 1;
+    }
+    float total = 0;
+    if (err == hipSuccess) err = hipEventElapsedTime(&total, profile.events[first], profile.events[first + launches]);
+    *call_ms += total;
+  }
+  release_events(profile);
+  if (err != hipSuccess) return hip_fail(err, "rg_profile_stop");
+  return RG_OK;
+}
+
+int rg_module_resident(const rg_module* module, int role, int64_t* blocks) {
+  if (!module || !blocks || role < 0 || role >= RG_ROLE_COUNT) return fail(RG_E_INVALID, "rg_module_resident: bad argument");
+  *blocks = module->resident[role];
+  return RG_OK;
+}
+
+int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, rg_plan* plan) {
+  if (!module || !plan) return fail(RG_E_INVALID, "rg_plan_create: null argument");
+  if (n < 0 || b < 0) return fail(RG_E_INVALID, "N and B must be nonnegative");
+  if (b == 0 && n != 0) return fail(RG_E_INVALID, "B=0 requires N=0");
+  if (schedule != RG_CLASSIFIED && schedule != RG_BLOCK_PER_SEGMENT) return fail(RG_E_INVALID, "unknown schedule");
+  if (schedule == RG_BLOCK_PER_SEGMENT && module->spec.debug_visits)
+    return fail(RG_E_INVALID, "debug visits require the classified schedule");
+  const rg_spec& spec = module->spec;
+  const int d = spec.feature_dim;
+  const Geometry& geo = module->geometry;
+  int64_t nd;
+  if (!mul_ok(n, d, &nd) || !mul_ok(nd, element_bytes(spec.dtype), &nd))
+    return fail(RG_E_INVALID, "N*D bytes overflow signed i64");
+  std::memset(plan, 0, sizeof *plan);
+  plan->schedule = schedule;
+  plan->n = n;
+  plan->b = b;
+  plan->t_wave = spec.t_wave;
+  plan->t_block = spec.t_block;
+  plan->part_rows = spec.part_rows;
+  plan->vec = geo.vec;
+  plan->flat = geo.flat ? 1 : 0;
+  if (b == 0) return RG_OK;
+
+  auto add_launch = [&](int role, int64_t gx, int64_t gy) {
+    const int i = plan->launches++;
+    plan->roles[i] = role;
+    plan->grid[i][0] = (uint32_t)std::min<int64_t>(std::max<int64_t>(gx, 1), kGridMax);
+    plan->grid[i][1] = (uint32_t)std::max<int64_t>(gy, 1);
+    plan->grid[i][2] = 1;
+    plan->block[i] = rg::kBlock;
+    plan->lds_bytes[i] = module->lds[role];
+  };
+  const int64_t tiles_block = feature_tiles(d, geo.vec, geo.flat, rg::kBlock);
+  const int64_t tiles_wave = feature_tiles(d, geo.vec, geo.flat, rg::kWave);
+  if (schedule == RG_BLOCK_PER_SEGMENT) {
+    add_launch(RG_ROLE_NAIVE, b, tiles_block);
+    return RG_OK;
+  }
+
+  // Workspace: every buffer at a 256-byte aligned offset of one allocation.
+  const int64_t b_split = std::min<int64_t>(b, n / (spec.t_block + 1));
+  const int64_t items_cap = b_split ? n / spec.part_rows + b_split : 0;
+  plan->b_split = b_split;
+  plan->items_cap = items_cap;
+  const bool softmax = spec.op == RG_OP_SOFTMAX;
+  int64_t sizes[RG_WORKSPACE_BUFFERS] = {0};
+  int64_t value;
+  sizes[RG_BUF_COUNTERS] = 4 * 8;
+  if (!mul_ok(b, 3 * 8, &value)) return fail(RG_E_INVALID, "queue bytes overflow");
+  sizes[RG_BUF_QUEUE] = value;
+  if (!mul_ok(items_cap, 8, &sizes[RG_BUF_ITEM_POS]) || !mul_ok(b_split, 8, &sizes[RG_BUF_PART_BEGIN]))
+    return fail(RG_E_INVALID, "split table bytes overflow");
+  int64_t stat_bytes, item_bytes;
+  if (!mul_ok(items_cap, (int64_t)d * 4, &item_bytes) || !mul_ok(b_split, (int64_t)d * 4, &stat_bytes))
+    return fail(RG_E_INVALID, "split workspace bytes overflow");
+  sizes[RG_BUF_PARTIALS] = item_bytes;
+  if (softmax) {
+    sizes[RG_BUF_PARTIAL_SUMS] = item_bytes;
+    sizes[RG_BUF_STATS_MAX] = stat_bytes;
+    sizes[RG_BUF_STATS_SUM] = stat_bytes;
+  }
+  if (spec.debug_visits && !mul_ok(b, 4, &sizes[RG_BUF_VISITS])) return fail(RG_E_INVALID, "visits bytes overflow");
+  int64_t end = 0;
+  for (int i = 0; i < RG_WORKSPACE_BUFFERS; ++i) {
+    const int64_t offset = (end + (int64_t)kAlign - 1) / (int64_t)kAlign * (int64_t)kAlign;
+    plan->buffer_offset[i] = (uint64_t)offset;
+    plan->buffer_bytes[i] = (uint64_t)sizes[i];
+    if (!add_ok(offset, sizes[i], &end)) return fail(RG_E_INVALID, "workspace bytes overflow signed i64");
+  }
+  plan->workspace_bytes = (uint64_t)end;
+
+  add_launch(RG_ROLE_INIT, 1, 1);
+  add_launch(RG_ROLE_CLASSIFY, (b + rg::kBlock - 1) / rg::kBlock, 1);
+  const int64_t wave_groups = (b + rg::kWavesPerBlock - 1) / rg::kWavesPerBlock;
+  add_launch(RG_ROLE_WAVE, std::min(module->resident[RG_ROLE_WAVE] / std::max<int64_t>(tiles_wave, 1), wave_groups),
+             tiles_wave);
+  add_launch(RG_ROLE_BLOCK, std::min(module->resident[RG_ROLE_BLOCK] / std::max<int64_t>(tiles_block, 1), b),
+             tiles_block);
+  if (b_split) {
+    add_launch(RG_ROLE_SPLIT_PARTIAL,
+               std::min(module->resident[RG_ROLE_SPLIT_PARTIAL] / std::max<int64_t>(tiles_block, 1), items_cap),
+               tiles_block);
+    const int64_t ft = combine_features_host(d);
+    const int64_t tiles_combine = (d + ft - 1) / ft;
+    add_launch(RG_ROLE_SPLIT_COMBINE,
+               std::min(module->resident[RG_ROLE_SPLIT_COMBINE] / std::max<int64_t>(tiles_combine, 1), b_split),
+               tiles_combine);
+    if (softmax)
+      add_launch(RG_ROLE_SPLIT_NORMALIZE,
+                 std::min(module->resident[RG_ROLE_SPLIT_NORMALIZE] / std::max<int64_t>(tiles_block, 1), items_cap),
+                 tiles_block);
+  }
+  return RG_OK;
+}
+
+int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets, void* out,
+           const float* mask, void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (!module || !plan) return fail(RG_E_INVALID, "rg_run: null module or plan");
+  const rg_spec& spec = module->spec;
+  if ((mask != nullptr) != (spec.has_mask != 0)) return fail(RG_E_INVALID, "mask presence must match the module");
+  if (plan->launches == 0) return RG_OK;
+  // N = 0 leaves values (and a softmax output) empty, possibly null.
+  if (!offsets || (plan->n > 0 && (!values || !out)) || (spec.op != RG_OP_SOFTMAX && !out))
+    return fail(RG_E_INVALID, "rg_run: null tensor pointer");
+  if (plan->workspace_bytes && (!workspace || workspace_bytes < plan->workspace_bytes))
+    return fail(RG_E_WORKSPACE, "workspace of %llu bytes is smaller than the plan's %llu",
+                (unsigned long long)workspace_bytes, (unsigned long long)plan->workspace_bytes);
+  rg::Params p;
+  std::memset(&p, 0, sizeof p);
+  p.values = values;
+  p.offsets = offsets;
+  p.out = out;
+  p.mask = mask;
+  p.n = plan->n;
+  p.b = plan->b;
+  p.d = spec.feature_dim;
+  p.scale = spec.scale;
+  p.has_scale = spec.scale != 1.0f;
+  p.t_wave = plan->t_wave;
+  p.t_block = plan->t_block;
+  p.part_rows = plan->part_rows;
+  p.items_cap = plan->items_cap;
+  p.b_split = plan->b_split;
+  p.min_len = -1;
+  p.max_len = -1;
+  char* base = static_cast<char*>(workspace);
+  auto buffer = [&](int index) -> void* {
+    return plan->buffer_bytes[index] ? base + plan->buffer_offset[index] : nullptr;
+  };
+  if (plan->schedule == RG_CLASSIFIED) {
+    p.counters = static_cast<int64_t*>(buffer(RG_BUF_COUNTERS));
+    p.queue = static_cast<int64_t*>(buffer(RG_BUF_QUEUE));
+    p.item_pos = static_cast<int64_t*>(buffer(RG_BUF_ITEM_POS));
+    p.part_begin = static_cast<int64_t*>(buffer(RG_BUF_PART_BEGIN));
+    p.partials = static_cast<float*>(buffer(RG_BUF_PARTIALS));
+    p.partial_sums = static_cast<float*>(buffer(RG_BUF_PARTIAL_SUMS));
+    p.stats_max = static_cast<float*>(buffer(RG_BUF_STATS_MAX));
+    p.stats_sum = static_cast<float*>(buffer(RG_BUF_STATS_SUM));
+    p.visits = static_cast<int32_t*>(buffer(RG_BUF_VISITS));
+  }
+  int previous = 0;
+  hipError_t err = hipGetDevice(&previous);
+  if (err == hipSuccess && previous != module->device) err = hipSetDevice(module->device);
+  if (err != hipSuccess) return hip_fail(err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Profile& profile = module->profile;
+  const bool record = profile.active && (int)profile.call_first.size() < profile.max_calls;
+  auto mark = [&]() {
+    hipEvent_t event;
+    if (err == hipSuccess) err = hipEventCreate(&event);
+    if (err == hipSuccess) {
+      profile.events.push_back(event);
+      err = hipEventRecord(event, s);
+    }
+  };
+  if (record) {
+    profile.call_first.push_back((int)profile.events.size());
+    profile.call_launches.push_back(plan->launches);
+    for (int i = 0; i < plan->launches; ++i) profile.call_roles.push_back(plan->roles[i]);
+  }
+  for (int i = 0; i < plan->launches && err == hipSuccess; ++i) {
+    const void* fn = module->roles[plan->roles[i]];
+    if (!fn) {
+      err = hipErrorInvalidDeviceFunction;
+      break;
+    }
+    if (record) mark();
+    p.tiles = (int32_t)plan->grid[i][1];
+    void* args[] = {&p};
+    if (err == hipSuccess)
+      err = hipLaunchKernel(fn, dim3(plan->grid[i][0], plan->grid[i][1], plan->grid[i][2]), dim3(plan->block[i]),
+                            args, 0, s);
+  }
+  if (record) mark();
+  if (previous != module->device) (void)hipSetDevice(previous);
+  if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
+  return RG_OK;
+}
+
+int rg_check_offsets(int device, int offsets_dtype, const void* offsets, int64_t n, int64_t b, int64_t min_len,
+                     int64_t max_len, int64_t* status, void* stream) {
+  if (!offsets || !status) return fail(RG_E_INVALID, "rg_check_offsets: null pointer");
+  if (offsets_dtype != RG_I32 && offsets_dtype != RG_I64) return fail(RG_E_INVALID, "offsets dtype must be i32 or i64");
+  if (n < 0 || b < 0 || b == kI64Max) return fail(RG_E_INVALID, "N and B must be nonnegative and B+1 representable");
+  rg::Params p;
+  std::memset(&p, 0, sizeof p);
+  p.offsets = offsets;
+  p.n = n;
+  p.b = b;
+  p.status = status;
+  p.min_len = min_len;
+  p.max_len = max_len;
+  int previous = 0;
+  hipError_t err = hipGetDevice(&previous);
+  if (err == hipSuccess && previous != device) err = hipSetDevice(device);
+  if (err != hipSuccess) return hip_fail(err, "hipSetDevice");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* args[] = {&p};
+  err = hipLaunchKernel(rg::kernel_offsets_init(), dim3(1), dim3(rg::kBlock), args, 0, s);
+  if (err == hipSuccess) {
+    const int64_t blocks = (b + 1 + rg::kBlock - 1) / rg::kBlock;
+    if (blocks > kGridMax) err = hipErrorInvalidValue;
+    else err = hipLaunchKernel(rg::kernel_offsets_check(offsets_dtype), dim3((uint32_t)blocks), dim3(rg::kBlock), args, 0, s);
+  }
+  if (previous != device) (void)hipSetDevice(previous);
+  if (err != hipSuccess) return hip_fail(err, "offsets check launch");
+  return RG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,305 @@
+// Device building blocks for segmented sum / max / softmax on CDNA4 (gfx950).
+//
+// Data layout: values is a packed row-major [N, D] array of f32 or bf16,
+// offsets is [B+1] i32/i64, out is [B, D] (sum, max) or [N, D] (softmax).
+// Reductions run along N per feature column in f32.
+//
+// Thread mapping. Every access is a vector of VEC adjacent elements (16 B
+// when the row allows it). Two mappings exist:
+//  * ROW  (VEC divides D): a row is read by LPR lanes (LPR = next power of
+//    two of D/VEC, capped by the group size G); the group covers G/LPR rows
+//    per step and lane (row_lane, feat_lane) owns features
+//    (tile*LPR + feat_lane)*VEC .. +VEC.
+//  * FLAT (D < VEC, D divides VEC): a segment's rows are a contiguous run of
+//    L*D elements, so the group reads it as a flat array of 16 B vectors,
+//    masking the partial vectors at either end. Component c of every vector
+//    belongs to feature c % D, so D=1 and D=2 still use full 16 B loads.
+// Reductions across lanes use xor butterflies within a wave64 and LDS only
+// across the waves of a workgroup.
+//
+// Numerics follow the reference's docs/semantics.md: f32 accumulation, sum
+// with per-lane compensated (Kahan) addition whose correction is cleared
+// when the total is not finite (ToGPU.cpp:377-387), max with IEEE maximum
+// (NaN propagates: v_maximum3_f32), softmax as exp(x - max) / sum with
+// -inf entries carrying zero mass and NaN / +inf / all -inf columns NaN.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rg {
+
+enum : int { OP_SUM = 0, OP_MAX = 1, OP_SOFTMAX = 2 };
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;            // threads of every workgroup-level worker
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kUnroll = 4;             // rows (or flat vectors) loaded per lane before folding
+constexpr int kCombineFeatures = 64;   // consecutive features per split-combine pass
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+__device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
+// IEEE-754 maximum: NaN if either operand is NaN (v_maximum3_f32 on gfx950).
+__device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
+
+// Everything a kernel needs, passed by value as the single kernel argument.
+struct Params {
+  const void* values;      // [N, D] f32 | bf16
+  const void* offsets;     // [B+1] i32 | i64
+  void* out;               // [B, D] or [N, D]
+  const float* mask;       // [N, D] f32 or null
+  int64_t n, b;
+  int32_t d;
+  float scale;
+  int32_t has_scale;
+  int32_t tiles;           // feature tiles of this launch (grid.y)
+  int64_t t_wave;          // longest segment of the wave class (rows)
+  int64_t t_block;         // longest segment of the block class (rows)
+  int64_t part_rows;       // rows per split part
+  int64_t items_cap;       // capacity of the split item tables
+  int64_t b_split;         // capacity of the split queue / statistics rows
+  int64_t* counters;       // [4]: wave, block, split segment counts; split items
+  int64_t* queue;          // [3, B] original segment ids per class
+  int64_t* item_pos;       // [items_cap] split-queue position of each item
+  int64_t* part_begin;     // [B] first item of each split-queue position
+  float* partials;         // [items_cap, D] part result / part softmax reference
+  float* partial_sums;     // [items_cap, D] part softmax mass
+  float* stats_max;        // [B_split, D] combined softmax reference
+  float* stats_sum;        // [B_split, D] combined softmax mass
+  int32_t* visits;         // [B] or null (debug)
+  int64_t* status;         // [7] checked-offsets status
+  int64_t min_len, max_len;  // checked-offsets hints, -1 when absent
+};
+
+// ---------------------------------------------------------------------------
+// Element access: VEC elements of T as f32.
+
+template <class T> struct Elem;
+
+template <> struct Elem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static float get(const float* p) { return *p; }
+  __device__ static void put(float* p, float v) { *p = v; }
+  template <int V>
+  __device__ static void load(const float* p, float (&x)[V]) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "unsupported vector width");
+    if constexpr (V == 8) {
+      float4 a = *reinterpret_cast<const float4*>(p), b = *reinterpret_cast<const float4*>(p + 4);
+      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+    } else if constexpr (V == 4) {
+      float4 r = *reinterpret_cast<const float4*>(p);
+      x[0] = r.x; x[1] = r.y; x[2] = r.z; x[3] = r.w;
+    } else if constexpr (V == 2) {
+      float2 r = *reinterpret_cast<const float2*>(p);
+      x[0] = r.x; x[1] = r.y;
+    } else {
+      x[0] = *p;
+    }
+  }
+  template <int V>
+  __device__ static void store(float* p, const float (&x)[V]) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "unsupported vector width");
+    if constexpr (V == 8) {
+      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+      *reinterpret_cast<float4*>(p + 4) = make_float4(x[4], x[5], x[6], x[7]);
+    } else if constexpr (V == 4) {
+      *reinterpret_cast<float4*>(p) = make_float4(x[0], x[1], x[2], x[3]);
+    } else if constexpr (V == 2) {
+      *reinterpret_cast<float2*>(p) = make_float2(x[0], x[1]);
+    } else {
+      *p = x[0];
+    }
+  }
+};
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// Round-to-nearest-even f32 -> bf16 pair (v_cvt_pk_bf16_f32), NaN stays NaN.
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  __bf16 a = (__bf16)lo, b = (__bf16)hi;
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+template <> struct Elem<__bf16> {
+  static constexpr int kBytes = 2;
+  __device__ static float get(const __bf16* p) {
+    return __uint_as_float((uint32_t)*reinterpret_cast<const uint16_t*>(p) << 16);
+  }
+  __device__ static void put(__bf16* p, float v) { *p = (__bf16)v; }
+  template <int V>
+  __device__ static void load(const __bf16* p, float (&x)[V]) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "unsupported vector width");
+    if constexpr (V == 8) {
+      uint4 r = *reinterpret_cast<const uint4*>(p);
+      x[0] = bf16_lo(r.x); x[1] = bf16_hi(r.x); x[2] = bf16_lo(r.y); x[3] = bf16_hi(r.y);
+      x[4] = bf16_lo(r.z); x[5] = bf16_hi(r.z); x[6] = bf16_lo(r.w); x[7] = bf16_hi(r.w);
+    } else if constexpr (V == 4) {
+      uint2 r = *reinterpret_cast<const uint2*>(p);
+      x[0] = bf16_lo(r.x); x[1] = bf16_hi(r.x); x[2] = bf16_lo(r.y); x[3] = bf16_hi(r.y);
+    } else if constexpr (V == 2) {
+      uint32_t r = *reinterpret_cast<const uint32_t*>(p);
+      x[0] = bf16_lo(r); x[1] = bf16_hi(r);
+    } else {
+      x[0] = get(p);
+    }
+  }
+  template <int V>
+  __device__ static void store(__bf16* p, const float (&x)[V]) {
+    if constexpr (V == 8) {
+      *reinterpret_cast<uint4*>(p) = make_uint4(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]),
+                                                pack_bf16(x[4], x[5]), pack_bf16(x[6], x[7]));
+    } else if constexpr (V == 4) {
+      *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16(x[0], x[1]), pack_bf16(x[2], x[3]));
+    } else if constexpr (V == 2) {
+      *reinterpret_cast<uint32_t*>(p) = pack_bf16(x[0], x[1]);
+    } else {
+      put(p, x[0]);
+    }
+  }
+};
+
+template <int V>
+__device__ __forceinline__ void load_mask(const float* p, float (&x)[V]) {
+  Elem<float>::load<V>(p, x);
+}
+
+template <class OffT>
+__device__ __forceinline__ int64_t offset_at(const Params& p, int64_t i) {
+  return (int64_t)static_cast<const OffT*>(p.offsets)[i];
+}
+
+// ---------------------------------------------------------------------------
+// Per-feature accumulation state.
+
+template <int OP> struct State;
+
+// Compensated sum (ToGPU.cpp:377-387): the correction is cleared whenever the
+// running total is not finite, so inf and NaN propagate unchanged.
+template <> struct State<OP_SUM> {
+  float s, c;
+  __device__ void init() { s = 0.f; c = 0.f; }
+  __device__ void fold(float x) {
+    float y = x - c;
+    float t = s + y;
+    float e = (t - s) - y;
+    c = __builtin_fabsf(t) < pos_inf() ? e : 0.f;
+    s = t;
+  }
+  __device__ float total() const { return s; }
+  __device__ void merge(const State& o) { s = s + o.s; c = 0.f; }
+  static constexpr float kIdentity = 0.f;
+};
+
+template <> struct State<OP_MAX> {
+  float m;
+  __device__ void init() { m = neg_inf(); }
+  __device__ void fold(float x) { m = fmax_nan(m, x); }
+  __device__ void merge(const State& o) { m = fmax_nan(m, o.m); }
+};
+
+// Softmax statistics: reference m and mass s = sum exp(x - m).
+// -inf entries carry no mass. NaN (IEEE maximum) or +inf (inf - inf) make s
+// NaN, which poisons the whole column as the contract requires.
+template <> struct State<OP_SOFTMAX> {
+  float m, s;
+  __device__ void init() { m = neg_inf(); s = 0.f; }
+  __device__ void fold(float x) {
+    float mn = fmax_nan(m, x);
+    float next = s * fast_exp(m - mn) + fast_exp(x - mn);
+    s = mn == neg_inf() ? s : next;
+    m = mn;
+  }
+  __device__ static float rescaled(float m, float s, float to) {
+    return m == neg_inf() ? s : s * fast_exp(m - to);
+  }
+  __device__ void merge(const State& o) {
+    float mn = fmax_nan(m, o.m);
+    s = rescaled(m, s, mn) + rescaled(o.m, o.s, mn);
+    m = mn;
+  }
+};
+
+template <int OP, int V>
+__device__ __forceinline__ void init_all(State<OP> (&st)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) st[v].init();
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane combination.
+
+template <int OP>
+__device__ __forceinline__ State<OP> shfl_xor(const State<OP>& a, int mask) {
+  State<OP> r;
+  if constexpr (OP == OP_SUM) {
+    r.s = __shfl_xor(a.s, mask, kWave);
+    r.c = 0.f;
+  } else if constexpr (OP == OP_MAX) {
+    r.m = __shfl_xor(a.m, mask, kWave);
+  } else {
+    r.m = __shfl_xor(a.m, mask, kWave);
+    r.s = __shfl_xor(a.s, mask, kWave);
+  }
+  return r;
+}
+
+// Combine lanes whose lane index agrees modulo `stride` (a power of two < 64):
+// afterwards every lane holds the combination over its residue class.
+template <int OP, int V>
+__device__ __forceinline__ void wave_reduce_stride(State<OP> (&st)[V], int stride) {
+  for (int mask = stride; mask < kWave; mask <<= 1) {
+#pragma unroll
+    for (int v = 0; v < V; ++v) st[v].merge(shfl_xor<OP>(st[v], mask));
+  }
+}
+
+template <int OP> struct Slots { static constexpr int kCount = OP == OP_SOFTMAX ? 2 : 1; };
+
+template <int OP>
+__device__ __forceinline__ void st_write(float* slot, int stride, const State<OP>& a) {
+  if constexpr (OP == OP_SUM) { slot[0] = a.s; }
+  else if constexpr (OP == OP_MAX) { slot[0] = a.m; }
+  else { slot[0] = a.m; slot[stride] = a.s; }
+}
+template <int OP>
+__device__ __forceinline__ State<OP> st_read(const float* slot, int stride) {
+  State<OP> a;
+  if constexpr (OP == OP_SUM) { a.s = slot[0]; a.c = 0.f; }
+  else if constexpr (OP == OP_MAX) { a.m = slot[0]; }
+  else { a.m = slot[0]; a.s = slot[stride]; }
+  return a;
+}
+
+// ---------------------------------------------------------------------------
+// Geometry of a group of G threads over a feature tile.
+
+struct RowGeo {
+  int lpr;          // lanes per row (power of two, <= G)
+  int rows_step;    // rows covered per step = G / lpr
+  int row_lane, feat_lane;
+  int feature;      // first feature of this lane
+  bool active;      // feature < D
+};
+
+// Lanes per row for D features read VEC at a time by a group of G threads.
+__device__ __forceinline__ int lanes_per_row(int d, int vec, int g) {
+  int lanes = (d + vec - 1) / vec;
+  int p = 1;
+  while (p < lanes && p < g) p <<= 1;
+  return p;
+}
+
+template <int VEC>
+__device__ __forceinline__ RowGeo row_geo(int d, int g, int t, int tile) {
+  RowGeo geo;
+  geo.lpr = lanes_per_row(d, VEC, g);
+  geo.rows_step = g / geo.lpr;
+  geo.row_lane = t / geo.lpr;
+  geo.feat_lane = t % geo.lpr;
+  geo.feature = (tile * geo.lpr + geo.feat_lane) * VEC;
+  geo.active = geo.feature < d;
+  return geo;
+}
+
+}  // namespace rg

@@ -1,0 +1,590 @@
+// Worker kernels for segmented sum / max / softmax on gfx950.
+//
+// Schedules (the same arithmetic in both):
+//  * block per segment ("naive"): grid.x walks segments, one 256-thread
+//    workgroup each (reference: the direct schedule, ToGPU.cpp:1283-1349).
+//  * classified: k_init + k_classify bin every segment by length into a
+//    wave64 queue, a workgroup queue and a split queue (reference:
+//    ToGPU.cpp:901-998, with wave64 thresholds); persistent workers drain
+//    each queue (ToGPU.cpp:999-1045). A split segment is cut into
+//    ceil(L / part_rows) parts -- proportional to its length instead of the
+//    reference's fixed 8 -- each processed by one workgroup; k_split_combine
+//    folds the parts (ToGPU.cpp:399-472) and, for softmax,
+//    k_split_normalize writes the probabilities (ToGPU.cpp:279-281).
+#pragma once
+
+#include "device.hpp"
+
+namespace rg {
+
+// ---------------------------------------------------------------------------
+// Input transformation: f32(value) * scale + mask (docs/mask-abi.md:28-43).
+
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void load_input(const Params& p, int64_t element, float (&x)[VEC]) {
+#pragma clang fp contract(off)
+  Elem<T>::template load<VEC>(static_cast<const T*>(p.values) + element, x);
+  if (p.has_scale) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = x[v] * p.scale;
+  }
+  if constexpr (MASK) {
+    float m[VEC];
+    load_mask<VEC>(p.mask + element, m);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = x[v] + m[v];
+  }
+}
+
+template <class T, bool MASK>
+__device__ __forceinline__ float load_input1(const Params& p, int64_t element) {
+#pragma clang fp contract(off)
+  float x = Elem<T>::get(static_cast<const T*>(p.values) + element);
+  if (p.has_scale) x = x * p.scale;
+  if constexpr (MASK) x = x + p.mask[element];
+  return x;
+}
+
+// Identity element a masked-off component folds in: it changes nothing.
+template <int OP> __device__ __forceinline__ float fold_identity() {
+  return OP == OP_SUM ? 0.f : neg_inf();
+}
+
+// ---------------------------------------------------------------------------
+// ROW mapping traversal of rows [r0, r1) by a group with geometry `g`.
+
+template <int OP, class T, int VEC, bool MASK>
+__device__ __forceinline__ void fold_rows(const Params& p, const RowGeo& g, int64_t r0, int64_t r1,
+                                          State<OP> (&st)[VEC]) {
+  if (!g.active) return;
+  const int64_t step = g.rows_step;
+  int64_t r = r0 + g.row_lane;
+  const int64_t d = p.d;
+  for (; r + (kUnroll - 1) * step < r1; r += kUnroll * step) {
+    float x[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) load_input<T, VEC, MASK>(p, (r + u * step) * d + g.feature, x[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) st[v].fold(x[u][v]);
+    }
+  }
+  for (; r < r1; r += step) {
+    float x[VEC];
+    load_input<T, VEC, MASK>(p, r * d + g.feature, x);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) st[v].fold(x[v]);
+  }
+}
+
+// Softmax normalisation of rows [r0, r1): out = exp(x - m) * (1 / s).
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void normalize_rows(const Params& p, const RowGeo& g, int64_t r0, int64_t r1,
+                                               const float (&m)[VEC], const float (&inv)[VEC]) {
+  if (!g.active) return;
+  const int64_t step = g.rows_step;
+  const int64_t d = p.d;
+  T* out = static_cast<T*>(p.out);
+  int64_t r = r0 + g.row_lane;
+  for (; r + (kUnroll - 1) * step < r1; r += kUnroll * step) {
+    float x[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) load_input<T, VEC, MASK>(p, (r + u * step) * d + g.feature, x[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) x[u][v] = fast_exp(x[u][v] - m[v]) * inv[v];
+      Elem<T>::template store<VEC>(out + (r + u * step) * d + g.feature, x[u]);
+    }
+  }
+  for (; r < r1; r += step) {
+    float x[VEC];
+    load_input<T, VEC, MASK>(p, r * d + g.feature, x);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) x[v] = fast_exp(x[v] - m[v]) * inv[v];
+    Elem<T>::template store<VEC>(out + r * d + g.feature, x);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FLAT mapping traversal of elements [lo, hi) (= rows [r0, r1) times D).
+// Vector j covers elements [j*VEC, j*VEC + VEC); component c is feature c % D.
+
+template <int OP, class T, int VEC, bool MASK>
+__device__ __forceinline__ void fold_flat(const Params& p, int g, int t, int64_t lo, int64_t hi,
+                                          State<OP> (&st)[VEC]) {
+  if (lo >= hi) return;
+  const int64_t full_lo = (lo + VEC - 1) / VEC, full_hi = hi / VEC;
+  // Up to two partial vectors: the one holding lo and the one holding hi-1.
+  const int64_t head = lo / VEC, tail = (hi - 1) / VEC;
+  const bool head_partial = lo % VEC != 0 || (head == tail && hi % VEC != 0);
+  const bool tail_partial = hi % VEC != 0 && tail != head;
+  if ((head_partial && t == 0) || (tail_partial && t == 1)) {
+    const int64_t j = t == 0 ? head : tail;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int64_t e = j * VEC + c;
+      st[c].fold(e >= lo && e < hi ? load_input1<T, MASK>(p, e) : fold_identity<OP>());
+    }
+  }
+  int64_t j = full_lo + t;
+  for (; j + (kUnroll - 1) * g < full_hi; j += kUnroll * g) {
+    float x[kUnroll][VEC];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) load_input<T, VEC, MASK>(p, (j + u * g) * VEC, x[u]);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) st[c].fold(x[u][c]);
+    }
+  }
+  for (; j < full_hi; j += g) {
+    float x[VEC];
+    load_input<T, VEC, MASK>(p, j * VEC, x);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) st[c].fold(x[c]);
+  }
+}
+
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void normalize_flat(const Params& p, int g, int t, int64_t lo, int64_t hi,
+                                               const float (&m)[VEC], const float (&inv)[VEC]) {
+  if (lo >= hi) return;
+  T* out = static_cast<T*>(p.out);
+  const int64_t full_lo = (lo + VEC - 1) / VEC, full_hi = hi / VEC;
+  const int64_t head = lo / VEC, tail = (hi - 1) / VEC;
+  const bool head_partial = lo % VEC != 0 || (head == tail && hi % VEC != 0);
+  const bool tail_partial = hi % VEC != 0 && tail != head;
+  if ((head_partial && t == 0) || (tail_partial && t == 1)) {
+    const int64_t j = t == 0 ? head : tail;
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int64_t e = j * VEC + c;
+      if (e >= lo && e < hi) Elem<T>::put(out + e, fast_exp(load_input1<T, MASK>(p, e) - m[c]) * inv[c]);
+    }
+  }
+  for (int64_t j = full_lo + t; j < full_hi; j += g) {
+    float x[VEC];
+    load_input<T, VEC, MASK>(p, j * VEC, x);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[c] = fast_exp(x[c] - m[c]) * inv[c];
+    Elem<T>::template store<VEC>(out + j * VEC, x);
+  }
+}
+
+// In FLAT mode component c holds feature c % D: fold components D.. into 0..D-1.
+template <int OP, int VEC>
+__device__ __forceinline__ void merge_components(State<OP> (&st)[VEC], int d) {
+#pragma unroll
+  for (int c = 1; c < VEC; ++c) {
+    if (c >= d) st[c % d].merge(st[c]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup reduction (G = kBlock) over lanes that share a feature lane:
+// lanes agree modulo `lpr`. Every thread ends with the total for its own
+// feature lane. `lds` holds kBlock * VEC * 2 floats.
+
+template <int OP, int VEC>
+__device__ __forceinline__ void block_reduce(State<OP> (&st)[VEC], int lpr, int feat_lane, float* lds) {
+  constexpr int S = Slots<OP>::kCount;
+  const int t = threadIdx.x, lane = t & (kWave - 1), w = t / kWave;
+  if (lpr < kWave) wave_reduce_stride<OP, VEC>(st, lpr);
+  const int rep = lpr < kWave ? lpr : kWave;
+  if (lane < rep) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) st_write<OP>(lds + ((w * kWave + lane) * VEC + v) * S, 1, st[v]);
+  }
+  __syncthreads();
+  State<OP> acc[VEC];
+  if (t < lpr) {
+    if (lpr <= kWave) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = st_read<OP>(lds + (t * VEC + v) * S, 1);
+      for (int ww = 1; ww < kWavesPerBlock; ++ww) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v].merge(st_read<OP>(lds + ((ww * kWave + t) * VEC + v) * S, 1));
+      }
+    } else {
+      const int wpr = lpr / kWave;              // waves per row
+      const int w0 = t / kWave, l0 = t & (kWave - 1);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) acc[v] = st_read<OP>(lds + ((w0 * kWave + l0) * VEC + v) * S, 1);
+      for (int ww = w0 + wpr; ww < kWavesPerBlock; ww += wpr) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v].merge(st_read<OP>(lds + ((ww * kWave + l0) * VEC + v) * S, 1));
+      }
+    }
+  }
+  __syncthreads();
+  if (t < lpr) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) st_write<OP>(lds + (t * VEC + v) * S, 1, acc[v]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) st[v] = st_read<OP>(lds + (feat_lane * VEC + v) * S, 1);
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Storing a reduction result / finishing softmax statistics.
+
+template <class T, int VEC>
+__device__ __forceinline__ void store_vec(T* dst, const float (&x)[VEC]) {
+  Elem<T>::template store<VEC>(dst, x);
+}
+
+template <int OP>
+__device__ __forceinline__ float value_of(const State<OP>& a) {
+  if constexpr (OP == OP_SUM) return a.s;
+  else return a.m;
+}
+
+template <int OP, int VEC>
+__device__ __forceinline__ void result_of(const State<OP> (&st)[VEC], float (&x)[VEC]) {
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    if constexpr (OP == OP_SUM) x[v] = st[v].s;
+    else x[v] = st[v].m;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void softmax_factors(const State<OP_SOFTMAX> (&st)[VEC], float (&m)[VEC],
+                                                float (&inv)[VEC]) {
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) {
+    m[v] = st[v].m;
+    inv[v] = 1.0f / st[v].s;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Whole-segment processing by a workgroup (block class, naive schedule) or
+// by one wave (wave class). `g` = group size, `t` = thread index in group.
+
+template <int OP, class T, int VEC, bool FLAT, bool MASK, bool BLOCK>
+__device__ __forceinline__ void process_segment(const Params& p, int64_t s, int64_t start, int64_t end,
+                                                int tile, float* lds) {
+  constexpr int G = BLOCK ? kBlock : kWave;
+  const int t = BLOCK ? threadIdx.x : (threadIdx.x & (kWave - 1));
+  State<OP> st[VEC];
+  init_all<OP, VEC>(st);
+  if constexpr (FLAT) {
+    const int64_t lo = start * p.d, hi = end * p.d;
+    fold_flat<OP, T, VEC, MASK>(p, G, t, lo, hi, st);
+    merge_components<OP, VEC>(st, p.d);
+    if constexpr (BLOCK) block_reduce<OP, VEC>(st, 1, 0, lds);
+    else wave_reduce_stride<OP, VEC>(st, 1);
+    if constexpr (OP == OP_SOFTMAX) {
+      float m[VEC], inv[VEC];
+      softmax_factors<VEC>(st, m, inv);
+      // Component c of every vector belongs to feature c % D.
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) { m[c] = m[c % p.d]; inv[c] = inv[c % p.d]; }
+      normalize_flat<T, VEC, MASK>(p, G, t, lo, hi, m, inv);
+    } else if (t == 0) {
+      float x[VEC];
+      result_of<OP, VEC>(st, x);
+      T* out = static_cast<T*>(p.out) + s * p.d;
+      for (int f = 0; f < p.d; ++f) Elem<T>::put(out + f, x[f]);
+    }
+  } else {
+    const RowGeo g = row_geo<VEC>(p.d, G, t, tile);
+    fold_rows<OP, T, VEC, MASK>(p, g, start, end, st);
+    if constexpr (BLOCK) block_reduce<OP, VEC>(st, g.lpr, g.feat_lane, lds);
+    else if (g.lpr < kWave) wave_reduce_stride<OP, VEC>(st, g.lpr);
+    if constexpr (OP == OP_SOFTMAX) {
+      float m[VEC], inv[VEC];
+      softmax_factors<VEC>(st, m, inv);
+      normalize_rows<T, VEC, MASK>(p, g, start, end, m, inv);
+    } else if (g.row_lane == 0 && g.active) {
+      float x[VEC];
+      result_of<OP, VEC>(st, x);
+      store_vec<T, VEC>(static_cast<T*>(p.out) + s * p.d + g.feature, x);
+    }
+  }
+  if (p.visits && tile == 0 && t == 0) atomicAdd(p.visits + s, 1);
+}
+
+template <class OffT>
+__device__ __forceinline__ void segment_rows(const Params& p, int64_t s, int64_t& start, int64_t& end) {
+  // Clamp to [0, N] so that offsets that break the (unchecked) validated
+  // contract can give wrong answers but never address outside values/out.
+  start = offset_at<OffT>(p, s);
+  end = offset_at<OffT>(p, s + 1);
+  start = start < 0 ? 0 : (start > p.n ? p.n : start);
+  end = end < start ? start : (end > p.n ? p.n : end);
+}
+
+// ---------------------------------------------------------------------------
+// Kernels.
+
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_naive(Params p) {
+  __shared__ float lds[kBlock * VEC * 2];
+  for (int64_t s = blockIdx.x; s < p.b; s += gridDim.x) {
+    int64_t start, end;
+    segment_rows<OffT>(p, s, start, end);
+    process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, blockIdx.y, lds);
+  }
+}
+
+// Wave-class worker: every wave drains queue 0 independently.
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_wave(Params p) {
+  const int64_t count = p.counters[0];
+  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
+  for (int64_t pos = (int64_t)blockIdx.x * kWavesPerBlock + threadIdx.x / kWave; pos < count; pos += stride) {
+    const int64_t s = p.queue[pos];
+    int64_t start, end;
+    segment_rows<OffT>(p, s, start, end);
+    process_segment<OP, T, VEC, FLAT, MASK, false>(p, s, start, end, blockIdx.y, nullptr);
+  }
+}
+
+// Block-class worker: every workgroup drains queue 1.
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_block(Params p) {
+  __shared__ float lds[kBlock * VEC * 2];
+  const int64_t count = p.counters[1];
+  for (int64_t pos = blockIdx.x; pos < count; pos += gridDim.x) {
+    const int64_t s = p.queue[p.b + pos];
+    int64_t start, end;
+    segment_rows<OffT>(p, s, start, end);
+    process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, blockIdx.y, lds);
+  }
+}
+
+// Rows of split item `item`: its part of its segment.
+template <class OffT>
+__device__ __forceinline__ void item_rows(const Params& p, int64_t item, int64_t& k, int64_t& s, int64_t& part,
+                                          int64_t& start, int64_t& end) {
+  k = p.item_pos[item];
+  s = p.queue[2 * p.b + k];
+  part = item - p.part_begin[k];
+  int64_t seg_start, seg_end;
+  segment_rows<OffT>(p, s, seg_start, seg_end);
+  start = seg_start + part * p.part_rows;
+  start = start > seg_end ? seg_end : start;
+  end = start + p.part_rows > seg_end ? seg_end : start + p.part_rows;
+}
+
+// One part of a split segment -> partials[item, :] (and partial_sums).
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_split_partial(Params p) {
+  __shared__ float lds[kBlock * VEC * 2];
+  const int64_t items = p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap;
+  const int t = threadIdx.x;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    int64_t k, s, part, start, end;
+    item_rows<OffT>(p, item, k, s, part, start, end);
+    State<OP> st[VEC];
+    init_all<OP, VEC>(st);
+    if constexpr (FLAT) {
+      fold_flat<OP, T, VEC, MASK>(p, kBlock, t, start * p.d, end * p.d, st);
+      merge_components<OP, VEC>(st, p.d);
+      block_reduce<OP, VEC>(st, 1, 0, lds);
+      if (t == 0) {
+        for (int f = 0; f < p.d; ++f) {
+          if constexpr (OP == OP_SUM) p.partials[item * p.d + f] = st[f].s;
+          else p.partials[item * p.d + f] = st[f].m;
+          if constexpr (OP == OP_SOFTMAX) p.partial_sums[item * p.d + f] = st[f].s;
+        }
+      }
+    } else {
+      const RowGeo g = row_geo<VEC>(p.d, kBlock, t, blockIdx.y);
+      fold_rows<OP, T, VEC, MASK>(p, g, start, end, st);
+      block_reduce<OP, VEC>(st, g.lpr, g.feat_lane, lds);
+      if (g.row_lane == 0 && g.active) {
+        float x[VEC];
+        result_of<OP, VEC>(st, x);
+        Elem<float>::store<VEC>(p.partials + item * p.d + g.feature, x);
+        if constexpr (OP == OP_SOFTMAX) {
+          float y[VEC];
+#pragma unroll
+          for (int v = 0; v < VEC; ++v) y[v] = st[v].s;
+          Elem<float>::store<VEC>(p.partial_sums + item * p.d + g.feature, y);
+        }
+      }
+    }
+  }
+}
+
+// Fold the parts of each split segment. Threads = part lanes x feature lanes
+// (kCombineFeatures consecutive features, coalesced); LDS tree over part lanes.
+__device__ __forceinline__ int combine_features(int d) {
+  int f = 1;
+  while (f < d && f < kCombineFeatures) f <<= 1;
+  return f;
+}
+
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_split_combine(Params p) {
+  __shared__ float lds[kBlock * 2];
+  constexpr int S = Slots<OP>::kCount;
+  const int ft = combine_features(p.d);
+  const int pl_count = kBlock / ft;
+  const int fl = threadIdx.x % ft, pl = threadIdx.x / ft;
+  const int64_t f = (int64_t)blockIdx.y * ft + fl;
+  const int64_t count = p.counters[2] < p.b_split ? p.counters[2] : p.b_split;
+  for (int64_t k = blockIdx.x; k < count; k += gridDim.x) {
+    const int64_t s = p.queue[2 * p.b + k];
+    int64_t start, end;
+    segment_rows<OffT>(p, s, start, end);
+    const int64_t parts = (end - start + p.part_rows - 1) / p.part_rows;
+    int64_t first = p.part_begin[k];
+    int64_t last = first + parts < p.items_cap ? first + parts : p.items_cap;
+    State<OP> acc;
+    acc.init();
+    if (f < p.d) {
+      for (int64_t item = first + pl; item < last; item += pl_count) {
+        if constexpr (OP == OP_SUM) {
+          acc.fold(p.partials[item * p.d + f]);
+        } else {
+          State<OP> part;
+          part.m = p.partials[item * p.d + f];
+          if constexpr (OP == OP_SOFTMAX) part.s = p.partial_sums[item * p.d + f];
+          acc.merge(part);
+        }
+      }
+    }
+    st_write<OP>(lds + threadIdx.x, kBlock, acc);
+    __syncthreads();
+    if (pl == 0) {
+      for (int q = 1; q < pl_count; ++q) acc.merge(st_read<OP>(lds + q * ft + fl, kBlock));
+      if (f < p.d) {
+        if constexpr (OP == OP_SOFTMAX) {
+          p.stats_max[k * p.d + f] = acc.m;
+          p.stats_sum[k * p.d + f] = acc.s;
+        } else {
+          Elem<T>::put(static_cast<T*>(p.out) + s * p.d + f, value_of<OP>(acc));
+        }
+      }
+      if constexpr (OP != OP_SOFTMAX) {
+        if (p.visits && blockIdx.y == 0 && threadIdx.x == 0) atomicAdd(p.visits + s, 1);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Softmax normalisation of each split part with the combined statistics.
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_split_normalize(Params p) {
+  const int64_t items = p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap;
+  const int t = threadIdx.x;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    int64_t k, s, part, start, end;
+    item_rows<OffT>(p, item, k, s, part, start, end);
+    float m[VEC], inv[VEC];
+    if constexpr (FLAT) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        const int f = c % p.d;
+        m[c] = p.stats_max[k * p.d + f];
+        inv[c] = 1.0f / p.stats_sum[k * p.d + f];
+      }
+      normalize_flat<T, VEC, MASK>(p, kBlock, t, start * p.d, end * p.d, m, inv);
+    } else {
+      const RowGeo g = row_geo<VEC>(p.d, kBlock, t, blockIdx.y);
+      if (g.active) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+          m[v] = p.stats_max[k * p.d + g.feature + v];
+          inv[v] = 1.0f / p.stats_sum[k * p.d + g.feature + v];
+        }
+        normalize_rows<T, VEC, MASK>(p, g, start, end, m, inv);
+      }
+    }
+    if (p.visits && part == 0 && blockIdx.y == 0 && t == 0) atomicAdd(p.visits + s, 1);
+  }
+}
+
+#ifdef RG_PROLOGUE_KERNELS
+// Defined in exactly one translation unit (kernels_common.hip).
+
+// Zero the class counters (and the debug visit counts).
+__global__ __launch_bounds__(kBlock) void k_init(Params p) {
+  if (threadIdx.x < 4) p.counters[threadIdx.x] = 0;
+  if (p.visits) {
+    for (int64_t s = threadIdx.x; s < p.b; s += kBlock) p.visits[s] = 0;
+  }
+}
+
+// Bin segments: wave (L <= t_wave), block (L <= t_block), split (longer).
+// Per wave and class: ballot, rank by mbcnt, one atomic add reserves the
+// wave's run of queue positions, so a wave's segments of one class sit in
+// consecutive positions in segment order (classified-abi.md:56-66).
+template <class OffT>
+__global__ __launch_bounds__(kBlock) void k_classify(Params p) {
+  const int64_t s = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool active = s < p.b;
+  int64_t length = 0;
+  if (active) {
+    int64_t start, end;
+    segment_rows<OffT>(p, s, start, end);
+    length = end - start;
+  }
+  const int cls = length <= p.t_wave ? 0 : (length <= p.t_block ? 1 : 2);
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    const bool mine = active && cls == c;
+    const uint64_t ballot = __ballot(mine);
+    if (ballot == 0) continue;
+    const int leader = __ffsll((unsigned long long)ballot) - 1;
+    int64_t base = 0;
+    if (lane == leader) base = (int64_t)atomicAdd((unsigned long long*)(p.counters + c), (unsigned long long)__popcll(ballot));
+    base = __shfl(base, leader, kWave);
+    if (mine) {
+      const int64_t pos = base + __popcll(ballot & below);
+      p.queue[c * p.b + pos] = s;
+      // Valid offsets never put more than b_split segments in the split
+      // queue; clamped invalid ones could, so never index past it.
+      if (c == 2 && pos < p.b_split) {
+        const int64_t parts = (length + p.part_rows - 1) / p.part_rows;
+        const int64_t first = (int64_t)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
+        p.part_begin[pos] = first;
+        // The host sizes the item table for any valid offsets; never write past it.
+        const int64_t last = first + parts < p.items_cap ? first + parts : p.items_cap;
+        for (int64_t i = first; i < last; ++i) p.item_pos[i] = pos;
+      }
+    }
+  }
+}
+
+// Checked mode (checked-abi.md): earliest offending index per condition.
+__global__ __launch_bounds__(kBlock) void k_offsets_init(Params p) {
+  if (threadIdx.x < 7) p.status[threadIdx.x] = INT64_MAX;
+}
+
+template <class OffT>
+__global__ __launch_bounds__(kBlock) void k_offsets_check(Params p) {
+  const int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (i > p.b) return;
+  long long* status = reinterpret_cast<long long*>(p.status);
+  const int64_t o = offset_at<OffT>(p, i);
+  if (i == 0 && o != 0) atomicMin(status + 0, 0ll);
+  if (i == p.b && o != p.n) atomicMin(status + 1, (long long)p.b);
+  if (o < 0) atomicMin(status + 2, (long long)i);
+  if (o > p.n) atomicMin(status + 3, (long long)i);
+  if (i < p.b) {
+    const int64_t next = offset_at<OffT>(p, i + 1);
+    if (next < o) {
+      atomicMin(status + 4, (long long)i);
+    } else if (o >= 0 && next <= p.n) {
+      const int64_t length = next - o;   // both ends in [0, N] and ordered: no overflow
+      if (p.min_len >= 0 && length < p.min_len) atomicMin(status + 5, (long long)i);
+      if (p.max_len >= 0 && length > p.max_len) atomicMin(status + 6, (long long)i);
+    }
+  }
+}
+
+#endif  // RG_PROLOGUE_KERNELS
+
+}  // namespace rg

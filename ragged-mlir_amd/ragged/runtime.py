@@ -1,0 +1,333 @@
+"""``CompiledProgram``: validate tensors and enqueue on the current HIP stream.
+
+Restates the public behaviour of the reference's ``python/ragged/runtime.py``
+(:218-558): ``run(values, offsets, out, stream=None, mode="validated", *,
+debug_buffers=None, mask=None, concurrent=True, select="auto", max_len=None)``
+validates every tensor before any allocation or launch, chooses a schedule
+per call with the cost model (``choose``), allocates one scratch buffer on
+the consumer stream, records the caller's tensors on that stream and makes a
+single native call that enqueues every kernel. Validated mode never
+synchronises; checked mode validates the offsets on the device first
+(docs/checked-abi.md). There is no CPU execution path: CPU tensors, a
+missing library or a non-gfx950 device raise ``RuntimeUnavailable``.
+"""
+from __future__ import annotations
+
+import importlib
+import json
+import threading
+import time
+from typing import Any
+
+from . import native
+from .cache import Artifact
+from .errors import CacheMismatch, RuntimeUnavailable, ValidationError
+from .model import ExecutionReport, ProgramSpec, canonical_json, runs_on
+from .selection import default_model
+from .validation import raise_for_status, validate_program
+
+_lock = threading.RLock()
+_modules: dict[tuple[int, str], native.NativeModule] = {}   # (device, artifact digest) -> module
+_device_arch: dict[int, str] = {}
+_device_l2_mib: dict[int, float | None] = {}
+I64_MAX = 2**63 - 1
+
+
+def _torch():
+    try:
+        return importlib.import_module("torch")
+    except ImportError as exc:
+        raise RuntimeUnavailable("PyTorch is not installed; install PyTorch-ROCm to execute") from exc
+
+
+def device_l2_mib(values) -> float | None:
+    """Total L2 (all XCDs) of the device holding ``values`` in MiB."""
+    device = getattr(values, "device", None)
+    if getattr(device, "type", None) != "cuda":
+        return None
+    index = device.index if device.index is not None else 0
+    if index not in _device_l2_mib:
+        try:
+            props = native.device_props(index)
+            _device_l2_mib[index] = props.l2_bytes * max(props.xcd_count, 1) / 2**20 if props.l2_bytes else None
+        except Exception:  # noqa: BLE001 - the cost model then uses its calibration value
+            _device_l2_mib[index] = None
+    return _device_l2_mib[index]
+
+
+def _overlaps(left, right) -> bool:
+    lstart, rstart = left.data_ptr(), right.data_ptr()
+    lend = lstart + left.numel() * left.element_size()
+    rend = rstart + right.numel() * right.element_size()
+    return lstart < rend and rstart < lend
+
+
+class CompiledProgram:
+    """A validated artifact plus, for adaptive programs, its block-per-segment
+    companion ``naive`` (reference runtime.py:218-268)."""
+
+    def __init__(self, spec: ProgramSpec, artifact: Artifact, *, cache_hit: bool = False,
+                 naive: "CompiledProgram | None" = None):
+        validate_program(spec, artifact)
+        self.spec, self.artifact, self.cache_hit = spec, artifact, cache_hit
+        self._metadata = json.loads(canonical_json(artifact.metadata))
+        self._digest = artifact.key.digest
+        self._selects = spec.strategy == "auto" and not spec.debug_visits and self._metadata["dispatch_abi"] is not None
+        self._schedule = "classified" if self._metadata["dispatch_abi"] is not None else "naive"
+        if naive is not None and (not self._selects or naive.spec != _naive_spec(spec)):
+            raise CacheMismatch("a block-per-segment companion must be the naive strategy of a classifying program")
+        self.naive = naive
+        self._choices: dict[tuple, tuple[str, dict[str, Any]]] = {}
+        self._plans: dict[tuple[int, int, int], native.Plan] = {}
+        self._names = {kernel["role"]: kernel["name"] for kernel in self._metadata["kernels"]}
+
+    @property
+    def selects(self) -> bool:
+        """Whether this program classifies on the device, so that one block per
+        segment is an alternative worth choosing per call."""
+        return self._selects
+
+    @property
+    def metadata(self) -> dict[str, Any]:
+        return self._metadata
+
+    def choose(self, n: int, b: int, max_len: int | None, l2_mib: float | None = None) -> tuple[str, dict[str, Any]]:
+        """The schedule ``run(select="auto")`` uses for this input, and why."""
+        if self.naive is None:
+            return self._schedule, {}
+        key = (n, b, max_len, l2_mib)
+        choice = self._choices.get(key)
+        if choice is None:
+            if len(self._choices) >= 256:
+                self._choices.clear()
+            element = 2 if self.spec.dtype == "bf16" else 4
+            choice = self._choices[key] = default_model().choose(self.spec.op, n, b, self.spec.feature_dim, max_len,
+                                                                 element, l2_mib=l2_mib)
+        return choice
+
+    def close(self) -> None:
+        """Drop this program's plans; the shared native module stays loaded."""
+        self._plans.clear()
+
+    # ------------------------------------------------------------------
+    def _validate_tensors(self, values, offsets, out, torch, *, checked: bool = False, mask=None) -> tuple[int, int]:
+        if self.spec.mask != (mask is not None):
+            raise ValidationError("mask presence must match the compiled specialization")
+        tensors = [("values", values), ("offsets", offsets), ("out", out)]
+        if mask is not None:
+            tensors.append(("mask", mask))
+        for name, tensor in tensors:
+            if not isinstance(tensor, torch.Tensor):
+                raise ValidationError(f"{name} must be a torch.Tensor")
+            if not tensor.is_cuda:
+                raise RuntimeUnavailable(f"{name} must be on a ROCm device that runs {self.spec.chip} code; "
+                                         "no CPU execution fallback exists")
+            if not tensor.is_contiguous():
+                raise ValidationError(f"{name} must be row-major contiguous")
+            if tensor.requires_grad:
+                raise ValidationError("autograd is outside the supported forward-only contract")
+        if values.device != offsets.device or values.device != out.device:
+            raise ValidationError("values, offsets and out must use the same device")
+        if values.ndim != 2 or values.shape[1] != self.spec.feature_dim:
+            raise ValidationError("values must have shape [N, static D]")
+        if offsets.ndim != 1 or offsets.numel() < 1:
+            raise ValidationError("offsets must have shape [B+1], including [0] when B=0")
+        dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[self.spec.dtype]
+        offset_dtype = {"i32": torch.int32, "i64": torch.int64}[self.spec.offsets_dtype]
+        if values.dtype != dtype or out.dtype != dtype or offsets.dtype != offset_dtype:
+            raise ValidationError("tensor dtype differs from compiled dtype/offsets specialization")
+        vector = self._metadata["d_vector"]
+        if vector > 1:
+            # Flat-mapped reductions store their [B, D] results element-wise.
+            scalar_out = self.spec.op != "softmax" and self._metadata["mapping"] == "flat"
+            for name, tensor in (("values", values), ("out", None if scalar_out else out), ("mask", mask)):
+                if tensor is not None and tensor.numel():
+                    need = min(16, vector * tensor.element_size())
+                    if tensor.data_ptr() % need:
+                        raise ValidationError(f"{name} must be {need}-byte aligned: this specialization accesses "
+                                              f"{vector} elements at a time (compile with vectorize=False for "
+                                              "unaligned views)")
+        n, b = values.shape[0], offsets.numel() - 1
+        if b == 0 and n != 0 and not checked:
+            raise ValidationError("B=0 requires N=0; values cannot exist without segments")
+        if self.spec.offsets_dtype == "i32" and n > 2**31 - 1:
+            raise ValidationError("N exceeds the i32 offsets range")
+        expected = (n if self.spec.op == "softmax" else b, self.spec.feature_dim)
+        if tuple(out.shape) != expected:
+            raise ValidationError(f"out shape must be {expected}")
+        if mask is not None:
+            if mask.dtype != torch.float32 or tuple(mask.shape) != tuple(values.shape):
+                raise ValidationError("mask must have f32 dtype and exactly values shape [N,D]; "
+                                      "broadcasting is unsupported")
+            if mask.device != values.device:
+                raise ValidationError("mask must use the values device")
+            if _overlaps(mask, out) or _overlaps(mask, offsets):
+                raise ValidationError("mask must not overlap out or offsets")
+        if _overlaps(offsets, values) or _overlaps(offsets, out):
+            raise ValidationError("offsets must not alias values or out")
+        overlap = values.numel() and out.numel() and _overlaps(values, out)
+        exact = values.data_ptr() == out.data_ptr() and tuple(values.shape) == tuple(out.shape)
+        if overlap:
+            if not exact or self.spec.alias != "inplace" or not self._metadata["alias_safe"]:
+                raise ValidationError("out aliases values without a safe in-place schedule")
+        elif self.spec.alias == "inplace" and not (exact or values.numel() == 0):
+            raise ValidationError("in-place specialization requires out and values to be the same buffer")
+        return n, b
+
+    def _module(self, device: int) -> native.NativeModule:
+        key = (device, self._digest)
+        with _lock:
+            module = _modules.get(key)
+            if module is None:
+                if self.artifact.key.library_sha256 != native.library_sha256():
+                    raise CacheMismatch("artifact was built for a different libragged_hip.so; recompile")
+                metadata = self._metadata
+                thresholds = metadata["thresholds"] or [-1, -1]
+                spec = native.make_spec(self.spec.op, self.spec.dtype, self.spec.offsets_dtype, self.spec.feature_dim,
+                                        scale=self.spec.scale, mask=self.spec.mask,
+                                        vectorize=self.spec.optimizations.vectorize,
+                                        debug_visits=self.spec.debug_visits, t_wave=thresholds[0],
+                                        t_block=thresholds[1], part_rows=metadata["part_rows"] or -1)
+                module = _modules[key] = native.NativeModule(device, spec)
+            return module
+
+    def _plan(self, module: native.NativeModule, n: int, b: int) -> native.Plan:
+        key = (module.device, n, b)
+        plan = self._plans.get(key)
+        if plan is None:
+            if len(self._plans) >= 256:
+                self._plans.clear()
+            plan = self._plans[key] = module.plan(n, b, self._schedule)
+        return plan
+
+    # ------------------------------------------------------------------
+    def run(self, values, offsets, out, stream=None, mode: str = "validated", *,
+            debug_buffers: dict[str, Any] | None = None, mask=None, concurrent: bool = True,
+            select: str = "auto", max_len: int | None = None) -> ExecutionReport:
+        """Enqueue on ``stream`` (default: the current stream of values' device).
+
+        ``select="auto"`` asks the cost model, given the longest segment
+        ``max_len`` when the caller knows it (a wrong value costs time, never
+        correctness); ``"classified"`` / ``"naive"`` force a schedule.
+        ``concurrent`` is accepted for compatibility: every class worker is
+        enqueued on the one stream, in a fixed order.
+        """
+        if select not in ("auto", "classified", "naive"):
+            raise ValidationError("select must be auto, classified or naive")
+        if max_len is not None and (type(max_len) is not int or max_len < 0):
+            raise ValidationError("max_len must be None or a nonnegative int")
+        if select == "naive" and self.naive is None:
+            raise ValidationError("select=naive requires a program compiled with a block-per-segment companion")
+        if self.naive is not None and select != "classified":
+            if select == "naive":
+                chosen, selection = "naive", {"forced": True}
+            else:
+                try:
+                    n, b = int(values.shape[0]), int(offsets.numel()) - 1
+                except (AttributeError, IndexError, TypeError):
+                    n = b = None
+                chosen, selection = (self.choose(n, b, max_len, device_l2_mib(values)) if n is not None
+                                     else ("classified", {}))
+            if chosen == "naive":
+                return self.naive._run(values, offsets, out, stream, mode, debug_buffers=debug_buffers, mask=mask,
+                                       selected="naive", selection=selection)
+        else:
+            selection = {"forced": True} if self.naive is not None else {}
+        return self._run(values, offsets, out, stream, mode, debug_buffers=debug_buffers, mask=mask,
+                         selected=self._schedule, selection=selection)
+
+    def _report(self, started, plan_names=(), grids=(), workspace=0, *, mode, selected, selection,
+                validation_bytes=0, validation_ms=None) -> ExecutionReport:
+        metadata = self._metadata
+        return ExecutionReport(
+            tuple(metadata["classes"]) if plan_names else (), tuple(metadata["thresholds"]), tuple(grids),
+            workspace + validation_bytes, self._digest, None, mode, tuple(plan_names),
+            (time.perf_counter() - started) * 1000, cache_hit=self.cache_hit,
+            validation_workspace_bytes=validation_bytes, validation_host_ms=validation_ms,
+            optimizations=metadata["optimizations"], d_tile=metadata["d_tile"], d_vector=metadata["d_vector"],
+            resources=None, streams=1, selected=selected, selection=selection)
+
+    def _run(self, values, offsets, out, stream, mode, *, debug_buffers, mask, selected, selection) -> ExecutionReport:
+        if mode not in ("validated", "checked"):
+            raise ValidationError("mode must be validated or checked")
+        if self.spec.mask != (mask is not None):
+            raise ValidationError("mask presence must match the compiled specialization")
+        if debug_buffers is not None and (type(debug_buffers) is not dict or debug_buffers
+                                          or not self.spec.debug_visits):
+            raise ValidationError("debug_buffers requires an empty dict and a debug_visits specialization")
+        torch = _torch()
+        checked = mode == "checked"
+        n, b = self._validate_tensors(values, offsets, out, torch, checked=checked, mask=mask)
+        started = time.perf_counter()
+        if b == 0 and not checked:
+            return self._report(started, mode=mode, selected=selected, selection=selection)
+        device = values.device.index if values.device.index is not None else torch.cuda.current_device()
+        with torch.cuda.device(device):
+            if device not in _device_arch:
+                _device_arch[device] = torch.cuda.get_device_properties(device).gcnArchName
+            if not runs_on(self.spec.chip, _device_arch[device]):
+                raise RuntimeUnavailable(f"compiled target {self.spec.chip} does not run on the current device "
+                                         f"({_device_arch[device]})")
+            active = stream if stream is not None else torch.cuda.current_stream(device)
+            if not isinstance(active, torch.cuda.Stream) or active.device != values.device:
+                raise ValidationError("stream must be a torch.cuda.Stream on the values device")
+            module = self._module(device)
+            names, grids, validation_bytes, validation_ms = [], [], 0, None
+            if checked:
+                validation_started = time.perf_counter()
+                with torch.cuda.stream(active):
+                    status = torch.empty((7,), dtype=torch.int64, device=values.device)
+                    host_status = torch.empty((7,), dtype=torch.int64, device="cpu", pin_memory=True)
+                    for tensor in (offsets, status):
+                        tensor.record_stream(active)
+                    native.check_offsets(device, self.spec.offsets_dtype, offsets.data_ptr(), n, b,
+                                         self.spec.hints.min_len, self.spec.hints.max_len, status.data_ptr(),
+                                         active.cuda_stream)
+                    host_status.copy_(status, non_blocking=True)
+                active.synchronize()
+                raise_for_status(host_status.tolist(), b=b)
+                validation_ms = (time.perf_counter() - validation_started) * 1000
+                validation_bytes = 56
+                names += ["ragged_0_offsets_init", "ragged_0_offsets_check"]
+                grids += [(1, 1, 1), (-(-(b + 1) // 256), 1, 1)]
+                if b == 0:
+                    return self._report(started, names, grids, 0, mode=mode, selected=selected, selection=selection,
+                                        validation_bytes=validation_bytes, validation_ms=validation_ms)
+            plan = self._plan(module, n, b)
+            workspace = None
+            if plan.workspace_bytes:
+                with torch.cuda.stream(active):
+                    workspace = torch.empty((plan.workspace_bytes,), dtype=torch.uint8, device=values.device)
+            inputs = [values, offsets, out] + ([mask] if mask is not None else [])
+            for tensor in inputs:
+                tensor.record_stream(active)
+            module.run(plan, values.data_ptr(), offsets.data_ptr(), out.data_ptr(),
+                       mask.data_ptr() if mask is not None else None,
+                       workspace.data_ptr() if workspace is not None else None, int(plan.workspace_bytes),
+                       active.cuda_stream)
+            for role, grid, _, _ in plan.steps:
+                names.append(self._kernel_name(role))
+                grids.append(grid)
+            if debug_buffers is not None and workspace is not None:
+                dtypes = {"class_counts": torch.int64, "segment_ids": torch.int64, "item_segments": torch.int64,
+                          "part_begin": torch.int64, "partials": torch.float32, "partial_sums": torch.float32,
+                          "max_stats": torch.float32, "sum_stats": torch.float32, "visits": torch.int32}
+                for name, offset, nbytes in plan.buffers:
+                    view = workspace[offset:offset + nbytes].view(dtypes[name])
+                    if name == "segment_ids":
+                        view = view.view(3, b)
+                    debug_buffers[name] = view
+        return self._report(started, names, grids, int(plan.workspace_bytes), mode=mode, selected=selected,
+                            selection=selection, validation_bytes=validation_bytes, validation_ms=validation_ms)
+
+    def _kernel_name(self, role: str) -> str:
+        phase = "online" if self.spec.op == "softmax" else self.spec.op
+        manifest_role = {"wave": f"wave_{phase}", "block": f"block_{phase}",
+                         "split_partial": f"split_partial_{phase}", "split_combine": f"split_combine_{phase}",
+                         "naive": phase}.get(role, role)
+        return self._names.get(manifest_role, f"ragged_0_{manifest_role}")
+
+
+def _naive_spec(spec: ProgramSpec) -> ProgramSpec:
+    from dataclasses import replace
+    return replace(spec, strategy="naive")

@@ -1,0 +1,113 @@
+"""Per-call choice between device classification and one block per segment.
+
+Same decision rule as the reference's ``python/ragged/selection.py``
+(:56-126): predict the complete-call time of each schedule from host-known
+statistics (N, B, D, element size and the caller's longest segment L) with a
+linear model per operation family {reduce, softmax} and schedule, and
+classify only when that is predicted faster by ``margin``; without L keep
+classification.
+
+The terms are re-derived for MI355X (model version 3, seven terms, µs):
+
+    t = c0 + c1*M + c2*S + c3*B/1000 + c4*M*log2(skew) + c5*X_l2 + c6*X_mall
+
+M = N*D / 2^18 elements; S = L*D*element_bytes / 2^20, the MiB the one
+workgroup that owns the longest segment must stream in block-per-segment;
+skew = L*B/N; X_l2 / X_mall = MiB of the call's working set (input rows plus
+output: B rows for sum/max, N for softmax) beyond the total L2 (8 XCDs x
+4 MiB) and beyond the 256 MiB Infinity Cache. The reference's single
+"beyond the 72 MiB L2" term becomes two because MI355X has two cache levels
+of very different size in front of HBM.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+import json
+import math
+from pathlib import Path
+from typing import Any
+
+from .errors import CacheMismatch
+
+MODEL_PATH = Path(__file__).with_name("cost_model.json")
+SCHEDULES = ("classified", "naive")
+FAMILIES = ("reduce", "softmax")
+TERMS = 7
+VERSION = 3
+
+
+def family(op: str) -> str:
+    return "softmax" if op == "softmax" else "reduce"
+
+
+def features(n: int, b: int, d: int, max_len: int, element_bytes: int = 4, op: str = "sum",
+             l2_mib: float = 32.0, mall_mib: float = 256.0) -> tuple[float, ...]:
+    """The seven prediction terms for one call."""
+    elements = n * d / 2**18
+    skew = max_len * b / n if n else 1.0
+    rows = n * d * element_bytes / 2**20
+    output_rows = n if op == "softmax" else b
+    working_set = rows + output_rows * d * element_bytes / 2**20
+    return (1.0, elements, max_len * d * element_bytes / 2**20, b / 1000.0,
+            elements * math.log2(max(1.0, skew)), max(0.0, working_set - l2_mib),
+            max(0.0, working_set - mall_mib))
+
+
+@dataclass(frozen=True)
+class CostModel:
+    coefficients: dict[str, dict[str, tuple[float, ...]]]
+    margin: float
+    calibration: dict[str, Any]
+    l2_mib: float = 32.0
+    mall_mib: float = 256.0
+
+    @classmethod
+    def from_dict(cls, data: dict[str, Any]) -> "CostModel":
+        try:
+            if data["version"] != VERSION:
+                raise CacheMismatch("unsupported cost model version")
+            coefficients = {name: {schedule: tuple(float(v) for v in data["coefficients"][name][schedule])
+                                   for schedule in SCHEDULES} for name in FAMILIES}
+            margin = float(data["margin"])
+            l2_mib, mall_mib = float(data["l2_mib"]), float(data["mall_mib"])
+        except (KeyError, TypeError, ValueError) as exc:
+            raise CacheMismatch(f"invalid cost model: {exc}") from exc
+        if (any(len(values) != TERMS or any(v < 0 or not math.isfinite(v) for v in values)
+                for schedules in coefficients.values() for values in schedules.values())
+                or not 0 <= margin < 1 or not l2_mib > 0 or not mall_mib > 0):
+            raise CacheMismatch(f"cost model coefficients must be {TERMS} nonnegative terms, margin in [0, 1) "
+                                "and positive cache capacities")
+        return cls(coefficients, margin, dict(data.get("calibration", {})), l2_mib, mall_mib)
+
+    @classmethod
+    def load(cls, path: Path = MODEL_PATH) -> "CostModel":
+        return cls.from_dict(json.loads(Path(path).read_text()))
+
+    def predict(self, schedule: str, op: str, n: int, b: int, d: int, max_len: int, element_bytes: int = 4,
+                l2_mib: float | None = None) -> float:
+        terms = features(n, b, d, max_len, element_bytes, op, self.l2_mib if l2_mib is None else l2_mib,
+                         self.mall_mib)
+        return sum(c * x for c, x in zip(self.coefficients[family(op)][schedule], terms))
+
+    def choose(self, op: str, n: int, b: int, d: int, max_len: int | None, element_bytes: int = 4,
+               l2_mib: float | None = None) -> tuple[str, dict[str, Any]]:
+        """The schedule to run and the inputs and predictions behind it."""
+        if max_len is None:
+            return "classified", {"max_len": None, "reason": "no length statistics on the host"}
+        if l2_mib is not None and not (isinstance(l2_mib, (int, float)) and l2_mib > 0):
+            raise ValueError("l2_mib must be a positive capacity in MiB")
+        classified = self.predict("classified", op, n, b, d, max_len, element_bytes, l2_mib)
+        naive = self.predict("naive", op, n, b, d, max_len, element_bytes, l2_mib)
+        selected = "classified" if classified < naive * (1 - self.margin) else "naive"
+        return selected, {"max_len": max_len, "l2_mib": self.l2_mib if l2_mib is None else l2_mib,
+                          "predicted_us": {"classified": round(classified, 2), "naive": round(naive, 2)}}
+
+
+_model: CostModel | None = None
+
+
+def default_model() -> CostModel:
+    global _model
+    if _model is None:
+        _model = CostModel.load()
+    return _model

@@ -1,0 +1,66 @@
+"""Write tests/golden/reference_cases.json from the reference's recorded runs.
+
+The reference (simon-jd/ragged-mlir) records, for every benchmark cell,
+the generator arguments and the sha256 of the generated lengths, offsets and
+values (``bench/run.py:51-65`` -> ``results/**/results.json`` "case" and
+"command"). Those records are data; this script copies the fields needed to
+pin ``ragged.workloads`` (the restated generators) into a small fixture. It
+reads JSON only and runs no reference code.
+
+Usage: python tests/golden/make_reference_cases.py [/root/reference]
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+import sys
+
+
+def _argument(command: list[str], flag: str, default=None):
+    if flag in command:
+        return command[command.index(flag) + 1]
+    return default
+
+
+def main(reference: Path) -> int:
+    cases: dict[tuple, dict] = {}
+    for path in sorted((reference / "results").rglob("results.json")):
+        try:
+            record = json.loads(path.read_text())
+        except (OSError, ValueError):
+            continue
+        case, command = record.get("case"), record.get("command")
+        if not isinstance(case, dict) or not isinstance(command, list):
+            continue
+        total = _argument(command, "--total-elements")
+        entry = {
+            "distribution": case["distribution"],
+            "segments": int(case["segments"]),
+            "total_elements": int(total) if total is not None else None,
+            "mean_length": int(_argument(command, "--mean-length", 64)),
+            "seed": int(case["seed"]),
+            "d": int(case["D"]),
+            "dtype": case["dtype"],
+            "offsets_dtype": case["offsets_dtype"],
+            "elements": int(case["elements"]),
+            "max_length": case["max_length"],
+            "histogram_counts": case["histogram_counts"],
+            "lengths_sha256": case["lengths_sha256"],
+            "offsets_sha256": case["offsets_sha256"],
+            "values_sha256": case["values_sha256"],
+            "source": str(path.relative_to(reference)),
+        }
+        key = (entry["distribution"], entry["segments"], entry["total_elements"], entry["mean_length"],
+               entry["seed"], entry["d"], entry["dtype"], entry["offsets_dtype"])
+        cases.setdefault(key, entry)
+    # Keep every distinct generator case whose values are cheap to regenerate.
+    chosen = sorted(cases.values(), key=lambda e: (e["elements"] * e["d"], e["source"]))
+    small = [e for e in chosen if e["elements"] * e["d"] <= 2**25]
+    out = Path(__file__).with_name("reference_cases.json")
+    out.write_text(json.dumps({"cases": small, "total_distinct": len(chosen)}, indent=1) + "\n")
+    print(f"wrote {len(small)} of {len(chosen)} distinct cases to {out}")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main(Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")))
