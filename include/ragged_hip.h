@@ -53,11 +53,13 @@ enum rg_role {
   RG_ROLE_SPLIT_COMBINE = 5,   /* fold the parts of each long segment */
   RG_ROLE_SPLIT_NORMALIZE = 6, /* softmax: normalise each part */
   RG_ROLE_NAIVE = 7,           /* block-per-segment schedule */
-  RG_ROLE_COUNT = 8
+  RG_ROLE_FUSED = 8,           /* softmax: register-resident worker over all block/split items */
+  RG_ROLE_DEFERRED = 9,        /* softmax: re-read pass for chunks that stopped waiting */
+  RG_ROLE_COUNT = 10
 };
 
 #define RG_MAX_LAUNCHES 8
-#define RG_WORKSPACE_BUFFERS 9
+#define RG_WORKSPACE_BUFFERS 13
 
 /* A kernel specialisation (ProgramSpec fields that change device code;
  * reference: python/ragged/model.py:129-188). */
@@ -106,11 +108,12 @@ typedef struct rg_plan {
   int64_t t_wave, t_block, part_rows;
   int32_t vec;                            /* elements per vector access */
   int32_t flat;                           /* 1: flat mapping (D < vec) */
+  int32_t fused;                          /* 1: softmax runs the register-resident worker */
 } rg_plan;
 
 /* Workspace buffer indices (rg_plan.buffer_offset / buffer_bytes). */
 enum rg_buffer {
-  RG_BUF_COUNTERS = 0,      /* i64[4] class counts and split items */
+  RG_BUF_COUNTERS = 0,      /* i64[8] class counts, split items, work ticket, deferred count */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class */
   RG_BUF_ITEM_POS = 2,      /* i64[items_cap] split position of each item */
   RG_BUF_PART_BEGIN = 3,    /* i64[B_split] first item of each split segment */
@@ -118,7 +121,11 @@ enum rg_buffer {
   RG_BUF_PARTIAL_SUMS = 5,  /* f32[items_cap, D] (softmax) */
   RG_BUF_STATS_MAX = 6,     /* f32[B_split, D] (softmax) */
   RG_BUF_STATS_SUM = 7,     /* f32[B_split, D] (softmax) */
-  RG_BUF_VISITS = 8         /* i32[B] (debug_visits) */
+  RG_BUF_VISITS = 8,        /* i32[B] (debug_visits) */
+  RG_BUF_DEFERRED = 9,      /* i64[items_cap] chunks left to the re-read pass (fused softmax) */
+  RG_BUF_ARRIVE = 10,       /* i32[items_cap] chunk arrivals per 32-chunk group (fused softmax) */
+  RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] group arrivals per split segment (fused softmax) */
+  RG_BUF_SEG_READY = 12     /* i32[B_split] statistics-published flags (fused softmax) */
 };
 
 typedef struct rg_module rg_module;
@@ -137,6 +144,10 @@ int rg_device_query(int ordinal, rg_device_props* out);
 
 /* Fill the default class thresholds and part size of `spec` (fields < 0). */
 int rg_spec_defaults(rg_spec* spec);
+
+/* 1 if `spec` (after defaults) runs softmax through the register-resident
+ * worker (RG_ROLE_FUSED), 0 if not, <0 on a bad spec. Host only. */
+int rg_spec_uses_fused(const rg_spec* spec);
 
 /* Create a kernel specialisation on a device; replaces
  * DriverModule(cubin, target) (Driver.h:23-27, Driver.cpp:178-195). Fails with
@@ -160,6 +171,12 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
  * (may be NULL when that is 0); `mask` is NULL unless the module has one. */
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
            void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* Longest wait, in microseconds, of a softmax chunk for the rest of its
+ * segment before it defers to the re-read pass (default 2000). A test and
+ * diagnostics control: 0 makes every chunk that finds its segment
+ * unfinished take the re-read path. */
+int rg_module_set_spin_limit(rg_module* module, int64_t microseconds);
 
 /* Measurement: while profiling is on, rg_run records a HIP event before
  * every launch and after the last one (no synchronisation), for at most

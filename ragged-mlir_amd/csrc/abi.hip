@@ -61,6 +61,20 @@ struct Geometry {
   int index;
 };
 
+// Rows one workgroup of the register-resident softmax holds, or 0 when the
+// specialisation has no such worker (flat mapping, or more than 256 lanes per
+// row). Mirrors fused_rows() and row_geo() of the device code.
+int64_t fused_capacity(int dtype, int d, int vec, bool flat, bool f32_logits) {
+  if (flat) return 0;
+  const int64_t lanes = (d + vec - 1) / vec;
+  if (lanes > rg::kBlock) return 0;
+  int lpr = 1;
+  while (lpr < lanes) lpr <<= 1;
+  const int store = (dtype == RG_F32 || f32_logits) ? 4 : 2;
+  const int rpt = std::min(32, 256 / (vec * store));
+  return (int64_t)(rg::kBlock / lpr) * rpt;
+}
+
 Geometry choose_geometry(int dtype, int d, bool vectorize) {
   const int widest = 16 / element_bytes(dtype);   // 4 f32 or 8 bf16 per 16 B
   if (!vectorize) return {1, false, 0};
@@ -110,6 +124,9 @@ struct rg_module {
   const void* roles[RG_ROLE_COUNT];
   int64_t resident[RG_ROLE_COUNT];
   uint32_t lds[RG_ROLE_COUNT];
+  bool fused;                 // softmax through k_softmax_fused (+ k_softmax_deferred)
+  int64_t spin_ticks;         // wall-clock ticks of a chunk's bounded wait
+  int64_t clock_khz;          // wall-clock rate
   mutable Profile profile;
 };
 
@@ -151,9 +168,34 @@ int rg_spec_defaults(rg_spec* spec) {
   if (spec->dtype != RG_F32 && spec->dtype != RG_BF16) return fail(RG_E_INVALID, "dtype must be f32 or bf16");
   const int64_t row = (int64_t)spec->feature_dim * element_bytes(spec->dtype);
   if (spec->t_wave < 0) spec->t_wave = std::max<int64_t>(1, kWaveBytes / row);
+  // Softmax with a register-resident worker: a block-class segment and a
+  // split chunk are exactly what one workgroup holds in registers.
+  const Geometry geo = choose_geometry(spec->dtype, spec->feature_dim, spec->vectorize != 0);
+  const int64_t capacity = spec->op == RG_OP_SOFTMAX
+      ? fused_capacity(spec->dtype, spec->feature_dim, geo.vec, geo.flat,
+                       spec->has_mask != 0 || spec->scale != 1.0f)
+      : 0;
+  if (capacity > spec->t_wave) {
+    if (spec->t_block < 0) spec->t_block = capacity;
+    if (spec->part_rows < 0) spec->part_rows = capacity;
+  }
   if (spec->t_block < 0) spec->t_block = std::max<int64_t>(spec->t_wave + 1, kBlockBytes / row);
   if (spec->part_rows < 0) spec->part_rows = std::max<int64_t>(1, kPartBytes / row);
   return RG_OK;
+}
+
+int rg_spec_uses_fused(const rg_spec* spec_in) {
+  if (!spec_in) return fail(RG_E_INVALID, "rg_spec_uses_fused: null spec");
+  rg_spec spec = *spec_in;
+  const int status = rg_spec_defaults(&spec);
+  if (status) return status;
+  if (spec.op != RG_OP_SOFTMAX) return 0;
+  // The register-resident softmax runs when one workgroup can hold a block
+  // segment and a split chunk.
+  const Geometry geo = choose_geometry(spec.dtype, spec.feature_dim, spec.vectorize != 0);
+  const int64_t capacity = fused_capacity(spec.dtype, spec.feature_dim, geo.vec, geo.flat,
+                                          spec.has_mask != 0 || spec.scale != 1.0f);
+  return capacity > 0 && spec.t_block <= capacity && spec.part_rows <= capacity ? 1 : 0;
 }
 
 int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
@@ -199,6 +241,11 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
   module->roles[RG_ROLE_SPLIT_COMBINE] = k.split_combine;
   module->roles[RG_ROLE_SPLIT_NORMALIZE] = k.split_normalize;
   module->roles[RG_ROLE_NAIVE] = k.naive;
+  const bool f32_logits = spec.has_mask != 0 || spec.scale != 1.0f;
+  const void* fused = f32_logits ? k.fused_f32 : k.fused;
+  module->fused = fused && k.deferred && rg_spec_uses_fused(&spec) == 1;
+  module->roles[RG_ROLE_FUSED] = module->fused ? fused : nullptr;
+  module->roles[RG_ROLE_DEFERRED] = module->fused ? k.deferred : nullptr;
 
   int previous = 0;
   err = hipGetDevice(&previous);
@@ -207,7 +254,12 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
     delete module;
     return hip_fail(err, "hipSetDevice");
   }
-  for (int role = 0; role < RG_ROLE_COUNT; ++role) {
+  int clock_khz = 0;
+  if (err == hipSuccess) err = hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device);
+  // A chunk waits at most 2 ms for the rest of its segment before deferring.
+  module->clock_khz = std::max(clock_khz, 1000);
+  module->spin_ticks = module->clock_khz * 2;
+  for (int role = 0; role < RG_ROLE_COUNT && err == hipSuccess; ++role) {
     module->resident[role] = 0;
     module->lds[role] = 0;
     if (!module->roles[role]) continue;
@@ -282,6 +334,13 @@ int rg_profile_stop(rg_module* module, double* role_ms, int64_t* role_launches, 
   return RG_OK;
 }
 
+int rg_module_set_spin_limit(rg_module* module, int64_t microseconds) {
+  if (!module || microseconds < 0 || microseconds > 10000000)
+    return fail(RG_E_INVALID, "rg_module_set_spin_limit: limit must be in [0, 10 s]");
+  module->spin_ticks = module->clock_khz * microseconds / 1000;
+  return RG_OK;
+}
+
 int rg_module_resident(const rg_module* module, int role, int64_t* blocks) {
   if (!module || !blocks || role < 0 || role >= RG_ROLE_COUNT) return fail(RG_E_INVALID, "rg_module_resident: bad argument");
   *blocks = module->resident[role];
@@ -336,7 +395,6 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   const bool softmax = spec.op == RG_OP_SOFTMAX;
   int64_t sizes[RG_WORKSPACE_BUFFERS] = {0};
   int64_t value;
-  sizes[RG_BUF_COUNTERS] = 4 * 8;
   if (!mul_ok(b, 3 * 8, &value)) return fail(RG_E_INVALID, "queue bytes overflow");
   sizes[RG_BUF_QUEUE] = value;
   if (!mul_ok(items_cap, 8, &sizes[RG_BUF_ITEM_POS]) || !mul_ok(b_split, 8, &sizes[RG_BUF_PART_BEGIN]))
@@ -350,6 +408,13 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     sizes[RG_BUF_STATS_MAX] = stat_bytes;
     sizes[RG_BUF_STATS_SUM] = stat_bytes;
   }
+  sizes[RG_BUF_COUNTERS] = 8 * 8;
+  if (module->fused && b_split) {
+    if (!mul_ok(items_cap, 8, &sizes[RG_BUF_DEFERRED]) || !mul_ok(items_cap, 4, &sizes[RG_BUF_ARRIVE]) ||
+        !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE]) || !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_READY]))
+      return fail(RG_E_INVALID, "fused softmax workspace bytes overflow");
+  }
+  plan->fused = module->fused ? 1 : 0;
   if (spec.debug_visits && !mul_ok(b, 4, &sizes[RG_BUF_VISITS])) return fail(RG_E_INVALID, "visits bytes overflow");
   int64_t end = 0;
   for (int i = 0; i < RG_WORKSPACE_BUFFERS; ++i) {
@@ -365,6 +430,11 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   const int64_t wave_groups = (b + rg::kWavesPerBlock - 1) / rg::kWavesPerBlock;
   add_launch(RG_ROLE_WAVE, std::min(module->resident[RG_ROLE_WAVE] / std::max<int64_t>(tiles_wave, 1), wave_groups),
              tiles_wave);
+  if (module->fused) {
+    add_launch(RG_ROLE_FUSED, std::min(module->resident[RG_ROLE_FUSED], b + items_cap), 1);
+    if (b_split) add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], items_cap), 1);
+    return RG_OK;
+  }
   add_launch(RG_ROLE_BLOCK, std::min(module->resident[RG_ROLE_BLOCK] / std::max<int64_t>(tiles_block, 1), b),
              tiles_block);
   if (b_split) {
@@ -428,6 +498,11 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
     p.stats_max = static_cast<float*>(buffer(RG_BUF_STATS_MAX));
     p.stats_sum = static_cast<float*>(buffer(RG_BUF_STATS_SUM));
     p.visits = static_cast<int32_t*>(buffer(RG_BUF_VISITS));
+    p.deferred = static_cast<int64_t*>(buffer(RG_BUF_DEFERRED));
+    p.arrive = static_cast<int32_t*>(buffer(RG_BUF_ARRIVE));
+    p.seg_arrive = static_cast<int32_t*>(buffer(RG_BUF_SEG_ARRIVE));
+    p.seg_ready = static_cast<int32_t*>(buffer(RG_BUF_SEG_READY));
+    p.spin_ticks = module->spin_ticks;
   }
   int previous = 0;
   hipError_t err = hipGetDevice(&previous);

@@ -59,7 +59,8 @@ struct Params {
   int64_t part_rows;       // rows per split part
   int64_t items_cap;       // capacity of the split item tables
   int64_t b_split;         // capacity of the split queue / statistics rows
-  int64_t* counters;       // [4]: wave, block, split segment counts; split items
+  int64_t* counters;       // [8]: wave, block, split segment counts; split items;
+                           //      work ticket; deferred chunks
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item
   int64_t* part_begin;     // [B] first item of each split-queue position
@@ -68,6 +69,11 @@ struct Params {
   float* stats_max;        // [B_split, D] combined softmax reference
   float* stats_sum;        // [B_split, D] combined softmax mass
   int32_t* visits;         // [B] or null (debug)
+  int64_t* deferred;       // [items_cap] chunks left to the re-read pass
+  int32_t* arrive;         // [items_cap] chunk arrivals per 32-chunk group (slot: group's first item)
+  int32_t* seg_arrive;     // [B_split] group arrivals per split segment
+  int32_t* seg_ready;      // [B_split] 1 once a split segment's statistics are published
+  int64_t spin_ticks;      // wall-clock ticks a chunk waits for its segment before deferring
   int64_t* status;         // [7] checked-offsets status
   int64_t min_len, max_len;  // checked-offsets hints, -1 when absent
 };
@@ -115,10 +121,12 @@ template <> struct Elem<float> {
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-// Round-to-nearest-even f32 -> bf16 pair (v_cvt_pk_bf16_f32), NaN stays NaN.
+// Round-to-nearest-even f32 -> bf16 pair in one v_cvt_pk_bf16_f32; NaN stays NaN.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  __bf16 a = (__bf16)lo, b = (__bf16)hi;
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  const f32x2_t pair = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(pair, bf16x2_t));
 }
 
 template <> struct Elem<__bf16> {

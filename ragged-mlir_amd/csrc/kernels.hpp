@@ -509,7 +509,7 @@ __global__ __launch_bounds__(kBlock) void k_split_normalize(Params p) {
 
 // Zero the class counters (and the debug visit counts).
 __global__ __launch_bounds__(kBlock) void k_init(Params p) {
-  if (threadIdx.x < 4) p.counters[threadIdx.x] = 0;
+  if (threadIdx.x < 8) p.counters[threadIdx.x] = 0;
   if (p.visits) {
     for (int64_t s = threadIdx.x; s < p.b; s += kBlock) p.visits[s] = 0;
   }
@@ -538,21 +538,36 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
     const uint64_t ballot = __ballot(mine);
     if (ballot == 0) continue;
     const int leader = __ffsll((unsigned long long)ballot) - 1;
-    int64_t base = 0;
-    if (lane == leader) base = (int64_t)atomicAdd((unsigned long long*)(p.counters + c), (unsigned long long)__popcll(ballot));
+    long long base = 0;
+    if (lane == leader) base = (long long)atomicAdd((unsigned long long*)(p.counters + c), (unsigned long long)__popcll(ballot));
     base = __shfl(base, leader, kWave);
-    if (mine) {
-      const int64_t pos = base + __popcll(ballot & below);
-      p.queue[c * p.b + pos] = s;
-      // Valid offsets never put more than b_split segments in the split
-      // queue; clamped invalid ones could, so never index past it.
-      if (c == 2 && pos < p.b_split) {
-        const int64_t parts = (length + p.part_rows - 1) / p.part_rows;
-        const int64_t first = (int64_t)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
-        p.part_begin[pos] = first;
-        // The host sizes the item table for any valid offsets; never write past it.
-        const int64_t last = first + parts < p.items_cap ? first + parts : p.items_cap;
-        for (int64_t i = first; i < last; ++i) p.item_pos[i] = pos;
+    const int64_t pos = base + __popcll(ballot & below);
+    if (mine) p.queue[c * p.b + pos] = s;
+    if (c != 2) continue;
+    // Split segments reserve ceil(L / part_rows) consecutive items. Valid
+    // offsets never put more than b_split segments in the split queue;
+    // clamped invalid ones could, so never index past it.
+    long long first = 0, parts = 0;
+    if (mine && pos < p.b_split) {
+      parts = (length + p.part_rows - 1) / p.part_rows;
+      first = (long long)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
+      p.part_begin[pos] = first;
+      if (p.seg_arrive) {
+        p.seg_arrive[pos] = 0;
+        p.seg_ready[pos] = 0;
+      }
+    }
+    // The whole wave writes each split segment's item entries.
+    uint64_t todo = __ballot(parts > 0);
+    while (todo) {
+      const int src = __ffsll((unsigned long long)todo) - 1;
+      todo &= todo - 1;
+      const long long f = __shfl(first, src, kWave), count = __shfl(parts, src, kWave);
+      const long long k = __shfl((long long)pos, src, kWave);
+      const int64_t last = f + count < p.items_cap ? f + count : p.items_cap;
+      for (int64_t i = f + lane; i < last; i += kWave) {
+        p.item_pos[i] = k;
+        if (p.arrive) p.arrive[i] = 0;
       }
     }
   }

@@ -5,6 +5,10 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
+#include "fused.hpp"
+
 namespace rg {
 
 struct KernelSet {
@@ -14,9 +18,45 @@ struct KernelSet {
   const void* split_partial;
   const void* split_combine;
   const void* split_normalize;   // softmax only
+  const void* fused;             // softmax, row mapping: register-resident worker
+  const void* fused_f32;         // same, storing f32 logits (scale or mask on bf16 input)
+  const void* deferred;          // softmax: re-read pass for chunks that stopped waiting
   int vec;                       // elements per vector access
   bool flat;                     // flat mapping (D < vec)
+  int rpt;                       // rows per thread of `fused` (0: no fused worker)
+  int rpt_f32;                   // rows per thread of `fused_f32`
 };
+
+// Rows per thread of the register-resident softmax: 256 bytes of row data
+// per thread (64 VGPRs), at most 32 rows.
+template <class S, int VEC>
+constexpr int fused_rows() {
+  return 256 / (VEC * (int)sizeof(S)) > 32 ? 32 : 256 / (VEC * (int)sizeof(S));
+}
+
+template <int OP, class T, class OFFT, int VEC, bool FLAT, bool MASK, bool STORE_F32>
+constexpr const void* fused_kernel() {
+  if constexpr (OP == OP_SOFTMAX && !FLAT && (STORE_F32 || !MASK)) {
+    using Store = typename std::conditional<STORE_F32, float, T>::type;
+    return (const void*)&k_softmax_fused<T, OFFT, VEC, fused_rows<Store, VEC>(), MASK, STORE_F32>;
+  } else {
+    return nullptr;
+  }
+}
+
+template <int OP, class T, class OFFT, int VEC, bool FLAT, bool MASK>
+constexpr const void* deferred_kernel() {
+  if constexpr (OP == OP_SOFTMAX && !FLAT) return (const void*)&k_softmax_deferred<T, OFFT, VEC, MASK>;
+  else return nullptr;
+}
+
+template <int OP, class T, int VEC, bool FLAT, bool MASK, bool STORE_F32>
+constexpr int fused_rpt() {
+  if constexpr (OP == OP_SOFTMAX && !FLAT && (STORE_F32 || !MASK))
+    return fused_rows<typename std::conditional<STORE_F32, float, T>::type, VEC>();
+  else
+    return 0;
+}
 
 // Geometry index: f32 -> 0:row1 1:row2 2:row4 3:flat4; bf16 -> 0:row1 1:row2 2:row4 3:row8 4:flat8.
 constexpr int kGeometries = 5;
@@ -40,13 +80,18 @@ const void* kernel_offsets_check(int offsets_dtype);
    (const void*)&rg::k_split_partial<OP, T, OFFT, VEC, FLAT, MASK>,                       \
    (const void*)&rg::k_split_combine<OP, T, OFFT, VEC, FLAT, MASK>,                       \
    OP == rg::OP_SOFTMAX ? (const void*)&rg::k_split_normalize<OP, T, OFFT, VEC, FLAT, MASK> : nullptr, \
-   VEC, FLAT}
+   rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, std::is_same<T, float>::value>(),              \
+   rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, true>(),                                       \
+   rg::deferred_kernel<OP, T, OFFT, VEC, FLAT, MASK>(),                                          \
+   VEC, FLAT,                                                                                    \
+   rg::fused_rpt<OP, T, VEC, FLAT, MASK, std::is_same<T, float>::value>(),                       \
+   rg::fused_rpt<OP, T, VEC, FLAT, MASK, true>()}
 
 // All geometries of one (op, offsets dtype, mask): f32 row then bf16 row.
 #define RG_GEOMETRIES(OP, OFFT, MASK)                                                           \
   {{RG_SET(OP, float, OFFT, 1, false, MASK), RG_SET(OP, float, OFFT, 2, false, MASK),          \
     RG_SET(OP, float, OFFT, 4, false, MASK), RG_SET(OP, float, OFFT, 4, true, MASK),           \
-    {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, false}},                          \
+    {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                          \
    {RG_SET(OP, __bf16, OFFT, 1, false, MASK), RG_SET(OP, __bf16, OFFT, 2, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 4, false, MASK), RG_SET(OP, __bf16, OFFT, 8, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 8, true, MASK)}}

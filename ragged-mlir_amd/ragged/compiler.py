@@ -101,6 +101,17 @@ class Compiler:
         metadata = build_manifest(spec, thresholds=(int(defaults.t_wave), int(defaults.t_block)),
                                   part_rows=int(defaults.part_rows), library_sha256=toolchain["library_sha256"],
                                   build_info=toolchain["build_info"])
+        if metadata["thresholds"]:
+            # Whether softmax runs register-resident depends on the effective
+            # thresholds (optimizations can move them).
+            effective = native.make_spec(spec.op, spec.dtype, spec.offsets_dtype, spec.feature_dim,
+                                         scale=spec.scale, mask=spec.mask, vectorize=spec.optimizations.vectorize,
+                                         debug_visits=spec.debug_visits, t_wave=metadata["thresholds"][0],
+                                         t_block=metadata["thresholds"][1], part_rows=metadata["part_rows"])
+            if native.uses_fused(effective):
+                metadata = build_manifest(spec, thresholds=tuple(metadata["thresholds"]),
+                                          part_rows=metadata["part_rows"], library_sha256=toolchain["library_sha256"],
+                                          build_info=toolchain["build_info"], fused=True)
         validate_manifest(metadata)
         code = (canonical_json({"library": native.LIBRARY_PATH.name, **toolchain}) + "\n").encode()
         # Bind the manifest to its source before publication.

@@ -23,9 +23,10 @@ OPS = {"sum": 0, "max": 1, "softmax": 2}
 DTYPES = {"f32": 0, "bf16": 1}
 INDEX_DTYPES = {"i32": 0, "i64": 1}
 SCHEDULES = {"classified": 0, "naive": 1}
-ROLES = ("init", "classify", "wave", "block", "split_partial", "split_combine", "split_normalize", "naive")
+ROLES = ("init", "classify", "wave", "block", "split_partial", "split_combine", "split_normalize", "naive",
+         "fused", "deferred")
 BUFFERS = ("class_counts", "segment_ids", "item_segments", "part_begin", "partials", "partial_sums",
-           "max_stats", "sum_stats", "visits")
+           "max_stats", "sum_stats", "visits", "deferred", "arrive", "segment_arrive", "segment_ready")
 MAX_LAUNCHES = 8
 
 RG_OK, RG_E_INVALID, RG_E_DEVICE, RG_E_UNSUPPORTED, RG_E_WORKSPACE = 0, -1, -2, -3, -4
@@ -52,7 +53,7 @@ class Plan(ctypes.Structure):
                 ("buffer_bytes", ctypes.c_uint64 * len(BUFFERS)), ("n", ctypes.c_int64), ("b", ctypes.c_int64),
                 ("b_split", ctypes.c_int64), ("items_cap", ctypes.c_int64), ("t_wave", ctypes.c_int64),
                 ("t_block", ctypes.c_int64), ("part_rows", ctypes.c_int64), ("vec", ctypes.c_int32),
-                ("flat", ctypes.c_int32)]
+                ("flat", ctypes.c_int32), ("fused", ctypes.c_int32)]
 
     @property
     def steps(self) -> list[tuple[str, tuple[int, int, int], int, int]]:
@@ -78,6 +79,7 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         "rg_last_error": (ctypes.c_char_p, []),
         "rg_device_query": (c_int, [c_int, ctypes.POINTER(DeviceProps)]),
         "rg_spec_defaults": (c_int, [ctypes.POINTER(Spec)]),
+        "rg_spec_uses_fused": (c_int, [ctypes.POINTER(Spec)]),
         "rg_module_create": (c_int, [c_int, ctypes.POINTER(Spec), ctypes.POINTER(vp)]),
         "rg_module_destroy": (None, [vp]),
         "rg_module_resident": (c_int, [vp, c_int, ctypes.POINTER(c_i64)]),
@@ -85,6 +87,7 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         "rg_run": (c_int, [vp, ctypes.POINTER(Plan), vp, vp, vp, vp, vp, c_u64, vp]),
         "rg_check_offsets": (c_int, [c_int, c_int, vp, c_i64, c_i64, c_i64, c_i64, vp, vp]),
         "rg_profile_start": (c_int, [vp, c_int]),
+        "rg_module_set_spin_limit": (c_int, [vp, c_i64]),
         "rg_profile_stop": (c_int, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64),
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64)]),
     }
@@ -148,6 +151,14 @@ def make_spec(op: str, dtype: str, offsets_dtype: str, feature_dim: int, *, scal
     return spec
 
 
+def uses_fused(spec: Spec) -> bool:
+    """Whether the library runs this softmax spec register-resident."""
+    status = library().rg_spec_uses_fused(ctypes.byref(spec))
+    if status < 0:
+        _check(status, "rg_spec_uses_fused")
+    return status == 1
+
+
 class NativeModule:
     """One kernel specialisation on one device (the reference's DriverModule)."""
 
@@ -174,6 +185,10 @@ class NativeModule:
             workspace_bytes: int, stream: int) -> None:
         _check(library().rg_run(self._handle, ctypes.byref(plan), values, offsets, out, mask, workspace,
                                 workspace_bytes, stream), "rg_run")
+
+    def set_spin_limit(self, microseconds: int) -> None:
+        """Bound of a softmax chunk's wait for its segment (test control)."""
+        _check(library().rg_module_set_spin_limit(self._handle, microseconds), "rg_module_set_spin_limit")
 
     def profile_start(self, max_calls: int) -> None:
         """Record per-launch HIP events in the next ``max_calls`` runs."""

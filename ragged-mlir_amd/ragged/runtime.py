@@ -311,7 +311,9 @@ class CompiledProgram:
             if debug_buffers is not None and workspace is not None:
                 dtypes = {"class_counts": torch.int64, "segment_ids": torch.int64, "item_segments": torch.int64,
                           "part_begin": torch.int64, "partials": torch.float32, "partial_sums": torch.float32,
-                          "max_stats": torch.float32, "sum_stats": torch.float32, "visits": torch.int32}
+                          "max_stats": torch.float32, "sum_stats": torch.float32, "visits": torch.int32,
+                          "deferred": torch.int64, "arrive": torch.int32, "segment_arrive": torch.int32,
+                          "segment_ready": torch.int32}
                 for name, offset, nbytes in plan.buffers:
                     view = workspace[offset:offset + nbytes].view(dtypes[name])
                     if name == "segment_ids":
@@ -324,7 +326,7 @@ class CompiledProgram:
         phase = "online" if self.spec.op == "softmax" else self.spec.op
         manifest_role = {"wave": f"wave_{phase}", "block": f"block_{phase}",
                          "split_partial": f"split_partial_{phase}", "split_combine": f"split_combine_{phase}",
-                         "naive": phase}.get(role, role)
+                         "naive": phase, "fused": "fused_online", "deferred": "deferred_online"}.get(role, role)
         return self._names.get(manifest_role, f"ragged_0_{manifest_role}")
 
 

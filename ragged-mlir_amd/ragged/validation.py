@@ -33,12 +33,16 @@ def _phase(op: str) -> str:
     return "online" if op == "softmax" else op
 
 
-def kernel_roles(spec: ProgramSpec, classes: list[str]) -> list[str]:
-    """Role names in launch order (reference naming, wave64 classes)."""
+def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> list[str]:
+    """Role names in launch order (reference naming, wave64 classes). With
+    ``fused`` the block and split classes of a softmax share one
+    register-resident worker plus its re-read pass."""
     phase = _phase(spec.op)
     if classes == ["block"] and spec.strategy == "naive":
         return [phase]
     roles = ["init", "classify"]
+    if fused:
+        return roles + [f"wave_{phase}", "fused_online", "deferred_online"]
     for segment_class in classes:
         if segment_class == "split":
             roles += [f"split_partial_{phase}", f"split_combine_{phase}"]
@@ -49,13 +53,13 @@ def kernel_roles(spec: ProgramSpec, classes: list[str]) -> list[str]:
     return roles
 
 
-def workspace_layout(spec: ProgramSpec, classified: bool) -> list[dict[str, Any]]:
+def workspace_layout(spec: ProgramSpec, classified: bool, fused: bool = False) -> list[dict[str, Any]]:
     """Symbolic workspace list; byte sizes are resolved per call by the
     library (rg_plan_create) from N and B."""
     if not classified:
         return []
     d = spec.feature_dim
-    workspace = [{"name": "class_counts", "dtype": "i64", "shape": [4]},
+    workspace = [{"name": "class_counts", "dtype": "i64", "shape": [8]},
                  {"name": "segment_ids", "dtype": "i64", "shape": [3, "B"]},
                  {"name": "item_segments", "dtype": "i64", "shape": ["items"]},
                  {"name": "part_begin", "dtype": "i64", "shape": ["B_split"]},
@@ -66,11 +70,16 @@ def workspace_layout(spec: ProgramSpec, classified: bool) -> list[dict[str, Any]
                       {"name": "sum_stats", "dtype": "f32", "shape": ["B_split", d]}]
     if spec.debug_visits:
         workspace.append({"name": "visits", "dtype": "i32", "shape": ["B"]})
+    if fused:
+        workspace += [{"name": "deferred", "dtype": "i64", "shape": ["items"]},
+                      {"name": "arrive", "dtype": "i32", "shape": ["items"]},
+                      {"name": "segment_arrive", "dtype": "i32", "shape": ["B_split"]},
+                      {"name": "segment_ready", "dtype": "i32", "shape": ["B_split"]}]
     return workspace
 
 
 def build_manifest(spec: ProgramSpec, *, thresholds: tuple[int, int], part_rows: int, library_sha256: str,
-                   build_info: str) -> dict[str, Any]:
+                   build_info: str, fused: bool = False) -> dict[str, Any]:
     """The manifest of ``spec`` for the library build ``library_sha256``."""
     options = spec.optimizations
     classified = spec.strategy == "auto" and options.classification
@@ -85,7 +94,8 @@ def build_manifest(spec: ProgramSpec, *, thresholds: tuple[int, int], part_rows:
     else:
         classes = ["block"]
     strategy_spec = spec if classified or spec.strategy == "naive" else _as_naive(spec)
-    roles = kernel_roles(strategy_spec, classes)
+    fused = bool(fused and classified and spec.op == "softmax")
+    roles = kernel_roles(strategy_spec, classes, fused)
     lpr, vec, mapping = options.geometry(spec.feature_dim, spec.dtype)
     effective = options.effective()
     effective["classification"] = classified
@@ -114,7 +124,8 @@ def build_manifest(spec: ProgramSpec, *, thresholds: tuple[int, int], part_rows:
         "mapping": mapping,
         "debug_visits": spec.debug_visits,
         "kernels": [{"role": role, "name": f"ragged_0_{role}", "block": [256, 1, 1]} for role in roles],
-        "workspace": workspace_layout(spec, classified),
+        "workspace": workspace_layout(spec, classified, fused),
+        "fused": fused,
         "library_sha256": library_sha256,
         "build_info": build_info,
         "optimizations": {"requested": options.to_dict(), "effective": effective},
@@ -206,10 +217,12 @@ def validate_program(spec: ProgramSpec, artifact: "Artifact", *, library_sha256:
         raise CacheMismatch("kernel manifest is not bound to the library build of its cache key")
     if library_sha256 is not None and key.library_sha256 != library_sha256:
         raise CacheMismatch("artifact was built for a different libragged_hip.so; recompile")
+    if type(metadata.get("fused")) is not bool:
+        raise CacheMismatch("fused must be boolean")
     expected = build_manifest(spec, thresholds=tuple(metadata["thresholds"]) if metadata["thresholds"] else (0, 1),
                               part_rows=metadata["part_rows"] or 1, library_sha256=key.library_sha256,
-                              build_info=key.build_info)
-    for name in ("kernels", "workspace", "classes", "d_vector", "mapping", "dispatch_abi", "fusion", "scale"):
+                              build_info=key.build_info, fused=metadata["fused"])
+    for name in ("kernels", "workspace", "classes", "d_vector", "mapping", "dispatch_abi", "fusion", "scale", "fused"):
         if metadata.get(name) != expected[name]:
             raise CacheMismatch(f"kernel manifest {name} differs from the source specialization")
     validation = metadata["validation"]

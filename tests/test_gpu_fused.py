@@ -1,0 +1,107 @@
+"""GPU tests of the register-resident softmax (k_softmax_fused): segments of
+many chunks (both merge levels), non-finite columns split across chunks, the
+bounded-wait fallback (k_softmax_deferred) forced from the host, and the
+debug queue/visit buffers."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from gpu_helpers import check, run_program
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("no ROCm device", allow_module_level=True)
+
+from ragged import Compiler, ProgramSpec  # noqa: E402
+from ragged.runtime import _modules  # noqa: E402
+from ragged.workloads import make_lengths, offsets_from_lengths  # noqa: E402
+
+
+def compile_softmax(cache, dtype, d, offsets_dtype="i64", **kwargs):
+    program = Compiler().compile(ProgramSpec("softmax", dtype, d, offsets_dtype, **kwargs), cache)
+    assert program.metadata["fused"], "expected the register-resident schedule"
+    return program
+
+
+def module_of(program):
+    return _modules[(0, program._digest)]
+
+
+@pytest.mark.parametrize("dtype,d,longest", [("bf16", 128, 100_000), ("f32", 128, 20_000), ("bf16", 64, 40_000),
+                                             ("f32", 16, 70_000), ("bf16", 256, 9_000), ("f32", 1024, 3_000)])
+def test_many_chunk_segments(artifact_cache, dtype, d, longest):
+    program = compile_softmax(artifact_cache, dtype, d)
+    lengths = np.array([3, longest, 0, 257, 1, longest // 3, 40, 4096, 5000, 12], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = (np.random.default_rng(d).normal(size=(int(offsets[-1]), d)) * 2).astype(np.float32)
+    actual, report = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified")
+    assert "ragged_0_fused_online" in report.kernel_names
+    check(actual, values, offsets, op="softmax", dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_nonfinite_columns_across_chunks(artifact_cache, dtype):
+    d = 16
+    program = compile_softmax(artifact_cache, dtype, d)
+    capacity = program.metadata["part_rows"]
+    lengths = np.array([5 * capacity + 7, capacity, 2 * capacity + 1, 3], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = np.random.default_rng(3).normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    first = lengths[0]
+    values[:first, 0] = -np.inf                    # all -inf over five chunks
+    values[:first:2, 1] = -np.inf                  # mixed
+    values[capacity * 3 + 5, 2] = np.inf           # +inf in one chunk poisons all
+    values[2, 3] = np.nan                          # NaN in the first chunk
+    values[first:first + capacity, 4] = -np.inf    # whole block segment column -inf
+    values[first + capacity:first + 2 * capacity, 5] = -np.inf   # one full chunk of -inf, others finite
+    actual, _ = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified")
+    check(actual, values, offsets, op="softmax", dtype=dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_deferred_path_matches(artifact_cache, dtype):
+    """With a zero wait limit almost every chunk of a long segment leaves its
+    registers and is normalised by the re-read pass; results are unchanged."""
+    d = 128
+    program = compile_softmax(artifact_cache, dtype, d)
+    lengths = make_lengths("long_tail", 200, seed=9, total_elements=60_000)
+    lengths[7] = 30_000
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = np.random.default_rng(5).normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    baseline, _ = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified")
+    module = module_of(program)
+    try:
+        module.set_spin_limit(0)
+        buffers = {}
+        actual, _ = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified")
+    finally:
+        module.set_spin_limit(2000)
+    check(actual, values, offsets, op="softmax", dtype=dtype)
+    # The deferred pass recomputes exp(x - M) / S directly: equal within the
+    # dtype's rounding, not bitwise.
+    np.testing.assert_allclose(actual, baseline, rtol=2e-2 if dtype == "bf16" else 1e-5, atol=1e-6)
+
+
+def test_debug_visits_and_queues(artifact_cache):
+    """Every segment's final output stage runs exactly once; queue membership
+    matches the length thresholds (reference test_classified.py:102-143)."""
+    d = 128
+    program = Compiler().compile(ProgramSpec("softmax", "bf16", d, "i64", debug_visits=True), artifact_cache)
+    thresholds = program.metadata["thresholds"]
+    lengths = np.array([0, 1, thresholds[0], thresholds[0] + 1, thresholds[1], thresholds[1] + 1,
+                        10 * thresholds[1], 33, 4097, 0], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = np.random.default_rng(1).normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    buffers = {}
+    actual, _ = run_program(program, values, offsets, dtype="bf16", op="softmax", debug_buffers=buffers)
+    check(actual, values, offsets, op="softmax", dtype="bf16")
+    counts = buffers["class_counts"].cpu().numpy()
+    classes = np.where(lengths <= thresholds[0], 0, np.where(lengths <= thresholds[1], 1, 2))
+    np.testing.assert_array_equal(counts[:3], np.bincount(classes, minlength=3))
+    ids = buffers["segment_ids"].cpu().numpy()
+    for c in range(3):
+        np.testing.assert_array_equal(np.sort(ids[c, :counts[c]]), np.flatnonzero(classes == c))
+    np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
