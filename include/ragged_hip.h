@@ -59,7 +59,7 @@ enum rg_role {
 };
 
 #define RG_MAX_LAUNCHES 8
-#define RG_WORKSPACE_BUFFERS 13
+#define RG_WORKSPACE_BUFFERS 16
 
 /* A kernel specialisation (ProgramSpec fields that change device code;
  * reference: python/ragged/model.py:129-188). */
@@ -125,7 +125,10 @@ enum rg_buffer {
   RG_BUF_DEFERRED = 9,      /* i64[items_cap] chunks left to the re-read pass (fused softmax) */
   RG_BUF_ARRIVE = 10,       /* i32[items_cap] chunk arrivals per 32-chunk group (fused softmax) */
   RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] group arrivals per split segment (fused softmax) */
-  RG_BUF_SEG_READY = 12     /* i32[B_split] statistics-published flags (fused softmax) */
+  RG_BUF_ITEMS = 12,        /* 32-byte descriptors [items_cap] of split chunks (fused softmax) */
+  RG_BUF_BLOCK_ITEMS = 13,  /* 32-byte descriptors [B] of whole segments (fused softmax) */
+  RG_BUF_PAIRS = 14,        /* u64[items_cap, D] published (max, sum) of each chunk (fused softmax) */
+  RG_BUF_FINAL_PAIRS = 15   /* u64[B_split, D] merged (max, sum) of long segments (fused softmax) */
 };
 
 typedef struct rg_module rg_module;
@@ -177,6 +180,19 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
  * diagnostics control: 0 makes every chunk that finds its segment
  * unfinished take the re-read path. */
 int rg_module_set_spin_limit(rg_module* module, int64_t microseconds);
+
+/* Diagnostics: a timeline of the register-resident softmax's work items.
+ * With `buffer` (device memory of `records` x 8 int64) set, every later run
+ * writes for each ticket t < records the record
+ *   {t, start, loaded, reduced, merged, end, hw_id, kind}
+ * (device wall-clock ticks at the item's start, after its loads and column
+ * max, after its column sums, after the segment merge, after its stores are
+ * issued; hw_id = __smid() of the workgroup; kind = 0 whole segment,
+ * 1 chunk merged directly, 2 chunk merged by tree, +4 when deferred, plus
+ * rows << 8). A null buffer turns it off. No counterpart in the reference:
+ * a measurement hook only. */
+int rg_module_set_trace(rg_module* module, void* buffer, int64_t records);
+int rg_device_clock_khz(int device, int64_t* khz);
 
 /* Measurement: while profiling is on, rg_run records a HIP event before
  * every launch and after the last one (no synchronisation), for at most

@@ -127,6 +127,8 @@ struct rg_module {
   bool fused;                 // softmax through k_softmax_fused (+ k_softmax_deferred)
   int64_t spin_ticks;         // wall-clock ticks of a chunk's bounded wait
   int64_t clock_khz;          // wall-clock rate
+  int64_t* trace;             // item timeline buffer (diagnostics) or null
+  int64_t trace_cap;
   mutable Profile profile;
 };
 
@@ -167,7 +169,8 @@ int rg_spec_defaults(rg_spec* spec) {
   if (spec->feature_dim < 1 || spec->feature_dim > 1024) return fail(RG_E_INVALID, "feature_dim must be in [1, 1024]");
   if (spec->dtype != RG_F32 && spec->dtype != RG_BF16) return fail(RG_E_INVALID, "dtype must be f32 or bf16");
   const int64_t row = (int64_t)spec->feature_dim * element_bytes(spec->dtype);
-  if (spec->t_wave < 0) spec->t_wave = std::max<int64_t>(1, kWaveBytes / row);
+  const bool default_wave = spec->t_wave < 0;
+  if (default_wave) spec->t_wave = std::max<int64_t>(1, kWaveBytes / row);
   // Softmax with a register-resident worker: a block-class segment and a
   // split chunk are exactly what one workgroup holds in registers.
   const Geometry geo = choose_geometry(spec->dtype, spec->feature_dim, spec->vectorize != 0);
@@ -175,7 +178,10 @@ int rg_spec_defaults(rg_spec* spec) {
       ? fused_capacity(spec->dtype, spec->feature_dim, geo.vec, geo.flat,
                        spec->has_mask != 0 || spec->scale != 1.0f)
       : 0;
-  if (capacity > spec->t_wave) {
+  if (capacity > 0) {
+    // The register-resident path has no wave class: t_wave 0 (empty
+    // segments only, which it also takes).
+    if (default_wave && spec->t_block < 0) spec->t_wave = 0;
     if (spec->t_block < 0) spec->t_block = capacity;
     if (spec->part_rows < 0) spec->part_rows = capacity;
   }
@@ -341,6 +347,23 @@ int rg_module_set_spin_limit(rg_module* module, int64_t microseconds) {
   return RG_OK;
 }
 
+int rg_module_set_trace(rg_module* module, void* buffer, int64_t records) {
+  if (!module || records < 0 || (buffer && records == 0))
+    return fail(RG_E_INVALID, "rg_module_set_trace: bad argument");
+  module->trace = static_cast<int64_t*>(buffer);
+  module->trace_cap = buffer ? records : 0;
+  return RG_OK;
+}
+
+int rg_device_clock_khz(int device, int64_t* khz) {
+  if (!khz) return fail(RG_E_INVALID, "rg_device_clock_khz: null argument");
+  int rate = 0;
+  const hipError_t err = hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, device);
+  if (err != hipSuccess) return hip_fail(err, "hipDeviceGetAttribute");
+  *khz = rate;
+  return RG_OK;
+}
+
 int rg_module_resident(const rg_module* module, int role, int64_t* blocks) {
   if (!module || !blocks || role < 0 || role >= RG_ROLE_COUNT) return fail(RG_E_INVALID, "rg_module_resident: bad argument");
   *blocks = module->resident[role];
@@ -402,16 +425,24 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   int64_t stat_bytes, item_bytes;
   if (!mul_ok(items_cap, (int64_t)d * 4, &item_bytes) || !mul_ok(b_split, (int64_t)d * 4, &stat_bytes))
     return fail(RG_E_INVALID, "split workspace bytes overflow");
-  sizes[RG_BUF_PARTIALS] = item_bytes;
-  if (softmax) {
-    sizes[RG_BUF_PARTIAL_SUMS] = item_bytes;
-    sizes[RG_BUF_STATS_MAX] = stat_bytes;
-    sizes[RG_BUF_STATS_SUM] = stat_bytes;
-  }
   sizes[RG_BUF_COUNTERS] = 8 * 8;
-  if (module->fused && b_split) {
-    if (!mul_ok(items_cap, 8, &sizes[RG_BUF_DEFERRED]) || !mul_ok(items_cap, 4, &sizes[RG_BUF_ARRIVE]) ||
-        !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE]) || !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_READY]))
+  if (!module->fused) {
+    sizes[RG_BUF_PARTIALS] = item_bytes;
+    if (softmax) {
+      sizes[RG_BUF_PARTIAL_SUMS] = item_bytes;
+      sizes[RG_BUF_STATS_MAX] = stat_bytes;
+      sizes[RG_BUF_STATS_SUM] = stat_bytes;
+    }
+  } else {
+    // Register-resident softmax: item descriptors, published (m, s) pairs
+    // and the merge counters; no item_pos / part_begin tables.
+    sizes[RG_BUF_ITEM_POS] = 0;
+    sizes[RG_BUF_PART_BEGIN] = 0;
+    if (!mul_ok(b, (int64_t)sizeof(rg::Item), &sizes[RG_BUF_BLOCK_ITEMS]) ||
+        !mul_ok(items_cap, (int64_t)sizeof(rg::Item), &sizes[RG_BUF_ITEMS]) ||
+        !mul_ok(items_cap, 8, &sizes[RG_BUF_DEFERRED]) || !mul_ok(items_cap, 4, &sizes[RG_BUF_ARRIVE]) ||
+        !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE]) || !mul_ok(item_bytes, 2, &sizes[RG_BUF_PAIRS]) ||
+        !mul_ok(stat_bytes, 2, &sizes[RG_BUF_FINAL_PAIRS]))
       return fail(RG_E_INVALID, "fused softmax workspace bytes overflow");
   }
   plan->fused = module->fused ? 1 : 0;
@@ -425,16 +456,19 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   }
   plan->workspace_bytes = (uint64_t)end;
 
-  add_launch(RG_ROLE_INIT, 1, 1);
+  // k_init is grid-stride: enough workgroups for the sentinel fill of the
+  // register-resident softmax (8 slots per thread), one for a plain reset.
+  const int64_t init_work = module->fused ? items_cap * d : 0;
+  add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, init_work / (rg::kBlock * 8))), 1);
   add_launch(RG_ROLE_CLASSIFY, (b + rg::kBlock - 1) / rg::kBlock, 1);
-  const int64_t wave_groups = (b + rg::kWavesPerBlock - 1) / rg::kWavesPerBlock;
-  add_launch(RG_ROLE_WAVE, std::min(module->resident[RG_ROLE_WAVE] / std::max<int64_t>(tiles_wave, 1), wave_groups),
-             tiles_wave);
   if (module->fused) {
     add_launch(RG_ROLE_FUSED, std::min(module->resident[RG_ROLE_FUSED], b + items_cap), 1);
     if (b_split) add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], items_cap), 1);
     return RG_OK;
   }
+  const int64_t wave_groups = (b + rg::kWavesPerBlock - 1) / rg::kWavesPerBlock;
+  add_launch(RG_ROLE_WAVE, std::min(module->resident[RG_ROLE_WAVE] / std::max<int64_t>(tiles_wave, 1), wave_groups),
+             tiles_wave);
   add_launch(RG_ROLE_BLOCK, std::min(module->resident[RG_ROLE_BLOCK] / std::max<int64_t>(tiles_block, 1), b),
              tiles_block);
   if (b_split) {
@@ -501,8 +535,16 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
     p.deferred = static_cast<int64_t*>(buffer(RG_BUF_DEFERRED));
     p.arrive = static_cast<int32_t*>(buffer(RG_BUF_ARRIVE));
     p.seg_arrive = static_cast<int32_t*>(buffer(RG_BUF_SEG_ARRIVE));
-    p.seg_ready = static_cast<int32_t*>(buffer(RG_BUF_SEG_READY));
+    p.items = static_cast<rg::Item*>(buffer(RG_BUF_ITEMS));
+    p.block_items = static_cast<rg::Item*>(buffer(RG_BUF_BLOCK_ITEMS));
+    p.pairs = static_cast<uint64_t*>(buffer(RG_BUF_PAIRS));
+    p.final_pairs = static_cast<uint64_t*>(buffer(RG_BUF_FINAL_PAIRS));
+    // A segment waits only if the grid can hold all its chunks at once; a
+    // margin of 1/8 covers workgroups that are slow to become resident.
+    p.wait_parts = std::max<int64_t>(1, module->resident[RG_ROLE_FUSED] * 7 / 8);
     p.spin_ticks = module->spin_ticks;
+    p.trace = module->trace;
+    p.trace_cap = module->trace_cap;
   }
   int previous = 0;
   hipError_t err = hipGetDevice(&previous);

@@ -36,12 +36,25 @@ constexpr int kBlock = 256;            // threads of every workgroup-level worke
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kUnroll = 4;             // rows (or flat vectors) loaded per lane before folding
 constexpr int kCombineFeatures = 64;   // consecutive features per split-combine pass
+constexpr int kDirect = 8;             // register-resident softmax: chunks merged by all-read
+constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 // IEEE-754 maximum: NaN if either operand is NaN (v_maximum3_f32 on gfx950).
 __device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
+
+// One work item of the register-resident softmax: a whole segment (k < 0)
+// or chunk c of `parts` of a long segment at split-queue position k.
+struct Item {
+  int64_t start;   // first row
+  int64_t seg;     // original segment id
+  int32_t rows;    // rows of the item
+  int32_t k;       // split-queue position, -1 for a whole segment
+  int32_t c;       // chunk index within the segment
+  int32_t parts;   // chunks of the segment
+};
 
 // Everything a kernel needs, passed by value as the single kernel argument.
 struct Params {
@@ -72,8 +85,14 @@ struct Params {
   int64_t* deferred;       // [items_cap] chunks left to the re-read pass
   int32_t* arrive;         // [items_cap] chunk arrivals per 32-chunk group (slot: group's first item)
   int32_t* seg_arrive;     // [B_split] group arrivals per split segment
-  int32_t* seg_ready;      // [B_split] 1 once a split segment's statistics are published
+  Item* items;             // [items_cap] split chunks (register-resident softmax)
+  Item* block_items;       // [B] whole segments (register-resident softmax)
+  uint64_t* pairs;         // [items_cap, D] published (m, s) of each chunk
+  uint64_t* final_pairs;   // [B_split, D] merged (M, S) of long split segments
   int64_t spin_ticks;      // wall-clock ticks a chunk waits for its segment before deferring
+  int64_t wait_parts;      // longest segment (in chunks) whose chunks wait for each other
+  int64_t* trace;          // [trace_cap, 8] item timeline or null (diagnostics)
+  int64_t trace_cap;
   int64_t* status;         // [7] checked-offsets status
   int64_t min_len, max_len;  // checked-offsets hints, -1 when absent
 };

@@ -1,24 +1,27 @@
 // Register-resident softmax: one persistent kernel over a dynamic queue of
 // work items, each read from HBM once and written once.
 //
-// Items (built by k_classify): every chunk of every split-class segment
-// (ceil(L / part_rows) chunks, contiguous in the queue), then every
-// block-class segment. A 256-thread workgroup takes the next item with one
-// atomic ticket and holds its rows in registers (RPT rows per thread):
+// Items (descriptors written by k_classify): every chunk of every
+// split-class segment (ceil(L / part_rows) chunks, contiguous in the queue),
+// then every block- and wave-class segment. A 256-thread workgroup takes the next item
+// with one atomic ticket (and prefetches the following descriptor while it
+// finishes) and holds its rows in registers (RPT rows per thread):
 //   1. m = column max of the rows (IEEE maximum: NaN propagates);
 //   2. e = exp(x - m) replaces x in registers, s = column sum of e;
 //   3. whole segment: y = e / s.  Chunk of a longer segment: publish (m, s),
 //      get the segment's merged (M, S) and write y = e * exp(m - M) / S.
-// Merging is deterministic: the last chunk to arrive in each group of 32
-// consecutive chunks folds the group in chunk order, and the last group to
-// arrive folds the groups in order and publishes (M, S). A chunk waits for
-// that with a bounded spin (relaxed agent-scope polling): since items
-// are dequeued in order, every chunk it waits for is already held by a
-// running workgroup whenever the device holds all chunks of the segment at
-// once. If the spin limit passes (a segment with more chunks than resident
-// workgroups, or a shared device), the chunk drops its registers and is
-// recorded for k_softmax_deferred, which re-reads it after this kernel.
-// No wait is unbounded.
+// Merging is deterministic (folds in chunk order). Up to kDirect chunks:
+// every chunk reads all published pairs itself. Longer: the last chunk of
+// each group of kGroup folds the group, the last group folds the groups and
+// publishes (M, S), and those segments are dequeued first. A chunk waits
+// for its segment with a bounded spin: since items are dequeued in order
+// and a workgroup holds an unstarted ticket only when it cannot wait or all
+// chunks of its segment are handed out, every chunk it waits for is started
+// by a running workgroup whenever the device holds all chunks of the
+// segment at once. Segments with more chunks than that (wait_parts), and
+// chunks whose spin limit passes, skip the wait: they drop their registers
+// and k_softmax_deferred re-reads them after this kernel. No wait is
+// unbounded.
 //
 // Reference semantics: docs/semantics.md (softmax row), the reference's
 // online statistics and merge algebra (ToGPU.cpp:486-557, 435-472) restated
@@ -144,94 +147,119 @@ __device__ __forceinline__ void block_allreduce(float (&v)[VEC], int lpr, int fe
 
 // Statistics shared between workgroups travel only through agent-scope
 // atomic stores and loads (coherent across the XCDs' L2 caches), so no
-// L2-wide writeback or invalidate is needed. A publisher waits until its
-// stores have completed (s_waitcnt vmcnt(0)) before the barrier after which
-// one thread bumps the counter that others test; readers issue their loads
-// only after observing that counter.
-__device__ __forceinline__ void store_agent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// L2-wide writeback or invalidate is needed. Each (m, s) pair of a feature is
+// one 64-bit store; k_classify fills every slot with a sentinel first (s bits
+// 0x7F800001, a signalling NaN, which f32 arithmetic never produces), so a
+// reader polls the data itself instead of a separate flag. A publisher that
+// bumps a counter waits for its stores to complete (s_waitcnt vmcnt(0))
+// before the barrier after which one thread updates the counter.
+__device__ __forceinline__ uint64_t pack_pair(float m, float s) {
+  return ((uint64_t)__float_as_uint(s) << 32) | __float_as_uint(m);
 }
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ float pair_m(uint64_t v) { return __uint_as_float((uint32_t)v); }
+__device__ __forceinline__ float pair_s(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
+__device__ __forceinline__ bool pair_ready(uint64_t v) { return (uint32_t)(v >> 32) != kSentinel; }
+__device__ __forceinline__ void store_pair(uint64_t* p, float m, float s) {
+  __hip_atomic_store(p, pack_pair(m, s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int load_agent(const int32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ uint64_t load_pair(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait for this wave's outstanding vector memory operations (vmcnt = 0).
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Fold statistics slots first, first + stride, ... (count of them, each D
-// floats of m and s) in order into (m, s) of feature f.
-__device__ __forceinline__ void fold_stats(const float* pm, const float* ps, int64_t first, int64_t count,
-                                           int64_t stride_items, int d, int f, float& m, float& s) {
+// Segments of at most kDirect chunks merge directly: every chunk reads all
+// chunks' pairs. Longer ones fold groups of kGroup chunks (last arriver) and
+// then the groups (last group), and publish (M, S) in final_pairs. Every
+// fold spreads features over all threads and keeps kDirect independent
+// loads in flight per thread, so it costs ceil(count / kDirect) round trips.
+
+// Fold slots base[0], base[stride * d], ... (count of them) of feature f, in
+// slot order; *ready is false if any slot still holds the sentinel.
+__device__ __forceinline__ State<OP_SOFTMAX> fold_slots(const uint64_t* base, int64_t count, int64_t stride, int d,
+                                                        int64_t f, bool* ready) {
   State<OP_SOFTMAX> acc;
   acc.init();
-  for (int64_t i = 0; i < count; ++i) {
-    State<OP_SOFTMAX> part;
-    const int64_t slot = (first + i * stride_items) * d + f;
-    part.m = load_agent(pm + slot);
-    part.s = load_agent(ps + slot);
-    acc.merge(part);
+  bool ok = true;
+  for (int64_t i0 = 0; i0 < count; i0 += kDirect) {
+    uint64_t v[kDirect];
+#pragma unroll
+    for (int j = 0; j < kDirect; ++j) v[j] = i0 + j < count ? load_pair(base + (i0 + j) * stride * d + f) : 0;
+#pragma unroll
+    for (int j = 0; j < kDirect; ++j) {
+      if (i0 + j < count) {
+        ok = ok && pair_ready(v[j]);
+        State<OP_SOFTMAX> part;
+        part.m = pair_m(v[j]);
+        part.s = pair_s(v[j]);
+        acc.merge(part);
+      }
+    }
   }
-  m = acc.m;
-  s = acc.s;
+  *ready = ok;
+  return acc;
 }
 
-// Chunk `item` (position c of P in its segment, first item F) has stored its
-// statistics (store_agent). Returns true once (M, S) of the segment is in
-// stats_max/stats_sum[k]; false if the spin limit passed first.
-__device__ bool merge_and_wait(const Params& p, int64_t item, int64_t k, int64_t first, int64_t parts, int* flag_s) {
+// Whole workgroup: fold `count` consecutive slots of every feature into
+// (lds_m[f], lds_s[f]). True, after a barrier, when no slot held the sentinel.
+__device__ __forceinline__ bool fold_to_lds(const uint64_t* base, int64_t count, int d, float* lds_m, float* lds_s) {
+  bool ok = true;
+  for (int f = threadIdx.x; f < d; f += kBlock) {
+    bool ready;
+    const State<OP_SOFTMAX> st = fold_slots(base, count, 1, d, f, &ready);
+    ok = ok && ready;
+    lds_m[f] = st.m;
+    lds_s[f] = st.s;
+  }
+  return __syncthreads_or(!ok) == 0;
+}
+
+// fold_to_lds until every slot is published or the wall-clock budget ends
+// (the decision is thread 0's, so the workgroup agrees); false on timeout.
+__device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, int d, int64_t spin_ticks,
+                                          float* lds_m, float* lds_s) {
+  const long long start = wall_clock64();
+  for (;;) {
+    if (fold_to_lds(base, count, d, lds_m, lds_s)) return true;
+    if (__syncthreads_or(threadIdx.x == 0 && wall_clock64() - start >= spin_ticks)) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Counter-based tree merge of a long segment: the last chunk of each group
+// folds the group into slot gfirst, the last group folds the groups into
+// final_pairs[k]. Never waits.
+__device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t k, int* flag_s) {
   const int t = threadIdx.x;
-  const int64_t c = item - first;
-  const int64_t group = c / kGroup;
+  const int64_t group = (slot - first) / kGroup;
   const int64_t gfirst = first + group * kGroup;
   const int64_t gsize = parts - group * kGroup < kGroup ? parts - group * kGroup : kGroup;
   const int64_t groups = (parts + kGroup - 1) / kGroup;
-  // Level 1: the last chunk of the group to arrive folds it into slot gfirst.
+  // Every read of *flag_s is followed by a barrier before its next write.
   wait_stores();
   __syncthreads();
   if (t == 0) *flag_s = atomicAdd(p.arrive + gfirst, 1) == gsize - 1;
   __syncthreads();
-  if (*flag_s) {
-    // Each thread owns features t, t+256, ...: it reads every slot of its
-    // features before overwriting slot gfirst.
-    for (int f = t; f < p.d; f += kBlock) {
-      float gm, gs;
-      fold_stats(p.partials, p.partial_sums, gfirst, gsize, 1, p.d, f, gm, gs);
-      store_agent(p.partials + gfirst * p.d + f, gm);
-      store_agent(p.partial_sums + gfirst * p.d + f, gs);
-    }
-    wait_stores();
-    __syncthreads();
-    // Level 2: the last group to arrive folds the groups and publishes.
-    if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == groups - 1;
-    __syncthreads();
-    if (*flag_s) {
-      for (int f = t; f < p.d; f += kBlock) {
-        float gm, gs;
-        fold_stats(p.partials, p.partial_sums, first, groups, kGroup, p.d, f, gm, gs);
-        store_agent(p.stats_max + k * p.d + f, gm);
-        store_agent(p.stats_sum + k * p.d + f, gs);
-      }
-      wait_stores();
-      __syncthreads();
-      if (t == 0) __hip_atomic_store(p.seg_ready + k, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-  // Wait for the segment's statistics (bounded).
-  if (t == 0) {
-    const long long start = wall_clock64();
-    int ready = load_agent(p.seg_ready + k);
-    while (!ready && wall_clock64() - start < p.spin_ticks) {
-      __builtin_amdgcn_s_sleep(2);
-      ready = load_agent(p.seg_ready + k);
-    }
-    *flag_s = ready;
-  }
+  const bool last_in_group = *flag_s != 0;
   __syncthreads();
-  const bool ready = *flag_s != 0;
+  if (!last_in_group) return;
+  for (int f = t; f < p.d; f += kBlock) {
+    bool ready;
+    const State<OP_SOFTMAX> g = fold_slots(p.pairs + gfirst * p.d, gsize, 1, p.d, f, &ready);
+    store_pair(p.pairs + gfirst * p.d + f, g.m, g.s);
+  }
+  wait_stores();
   __syncthreads();
-  return ready;
+  if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == groups - 1;
+  __syncthreads();
+  const bool last_group = *flag_s != 0;
+  __syncthreads();
+  if (!last_group) return;
+  for (int f = t; f < p.d; f += kBlock) {
+    bool ready;
+    const State<OP_SOFTMAX> g = fold_slots(p.pairs + first * p.d, groups, kGroup, p.d, f, &ready);
+    store_pair(p.final_pairs + k * p.d + f, g.m, g.s);
+  }
 }
 
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
@@ -241,45 +269,61 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   using Store = typename std::conditional<STORE_F32, float, T>::type;
   using In = Words<T, VEC>;
   using Reg = Words<Store, VEC>;
+  // lds: reductions, then the segment's merged max per feature; lds_s: its sum.
   __shared__ float lds[kBlock * VEC];
-  __shared__ int64_t ticket_s;
+  __shared__ float lds_s[kBlock * VEC];
+  __shared__ int64_t next_s;
   __shared__ int flag_s;
+  __shared__ int64_t stamp_s[5];    // item timeline (diagnostics), thread 0 only
   const int t = threadIdx.x;
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
-  const int64_t n_split = p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap;
+  // Ticket order: chunks of segments merged by tree (top of the item
+  // array), chunks of segments merged directly (bottom), block-class
+  // segments, wave-class segments (far end of block_items).
+  const int64_t n_tree = p.counters[6] < p.items_cap ? p.counters[6] : p.items_cap;
+  const int64_t n_direct = p.counters[3] < p.items_cap - n_tree ? p.counters[3] : p.items_cap - n_tree;
+  const int64_t n_split = n_tree + n_direct;
   const int64_t n_block = p.counters[1];
-  const int64_t total = n_split + n_block;
+  const int64_t total = n_split + n_block + p.counters[0];
   const int64_t d = p.d;
-  // Byte offsets inside a chunk: per thread, and the stride between a
+  // Byte offsets inside an item: per thread, and the stride between a
   // thread's rows.
   const int voff_in = g.active ? (g.row_lane * p.d + g.feature) * (int)sizeof(T) : kOutOfRange;
   const int step_in = g.rows_step * p.d * (int)sizeof(T);
   const int voff_mask = g.active ? (g.row_lane * p.d + g.feature) * 4 : kOutOfRange;
   const int step_mask = g.rows_step * p.d * 4;
-  for (;;) {
-    if (t == 0) ticket_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+  const bool publisher = g.row_lane == 0 && g.active;   // one thread per feature group
+  // Index of a chunk ticket in the item (and pair) arrays.
+  auto index_of = [&](int64_t ticket) -> int64_t {
+    return ticket < n_tree ? p.items_cap - n_tree + ticket : ticket - n_tree;
+  };
+  auto item_at = [&](int64_t ticket) -> Item {
+    if (ticket < n_split) return p.items[index_of(ticket)];
+    if (ticket < n_split + n_block) return p.block_items[ticket - n_split];
+    return p.block_items[p.b - 1 - (ticket - n_split - n_block)];
+  };
+  if (t == 0) next_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+  __syncthreads();
+  int64_t ticket = next_s;
+  Item it;
+  if (ticket < total) it = item_at(ticket);
+  while (ticket < total) {
+    const bool chunk = it.k >= 0;
+    const bool may_wait = chunk && it.parts <= p.wait_parts;
+    // Next ticket: taken while this item loads once every chunk has been
+    // handed out (this ticket is past them), else when this item starts its
+    // stores. Chunks of one segment therefore start together, and a ticket
+    // held but not started never belongs to a segment its holder waits for:
+    // waits only run down to chunks that are started.
+    const bool early = ticket >= n_split;
     __syncthreads();
-    const int64_t ticket = ticket_s;
-    __syncthreads();
-    if (ticket >= total) break;
-    int64_t s, k = -1, first = 0, parts = 1, start, end;
-    const bool chunk = ticket < n_split;
-    if (chunk) {
-      int64_t part;
-      item_rows<OffT>(p, ticket, k, s, part, start, end);
-      first = p.part_begin[k];
-      int64_t seg_start, seg_end;
-      segment_rows<OffT>(p, s, seg_start, seg_end);
-      parts = (seg_end - seg_start + p.part_rows - 1) / p.part_rows;
-    } else {
-      s = p.queue[p.b + (ticket - n_split)];
-      segment_rows<OffT>(p, s, start, end);
-    }
-    const int rows = (int)(end - start);   // at most one chunk: fits a workgroup's registers
+    unsigned long long taken = 0;
+    if (t == 0 && early) taken = atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+    const bool tracing = p.trace && ticket < p.trace_cap;
+    if (tracing && t == 0) stamp_s[0] = wall_clock64();
+    const int rows = it.rows;
+    const int64_t start = it.start;
     const int64_t chunk_elems = (int64_t)rows * d;
-    // Per-item copies of the offsets: computing each row's offset next to
-    // its access (instead of hoisting RPT offsets out of the item loop)
-    // keeps them out of the register budget.
     int voff = voff_in, voff_m = voff_mask;
     asm volatile("" : "+v"(voff), "+v"(voff_m));
     const Rsrc in = make_rsrc(static_cast<const T*>(p.values) + start * d, chunk_elems * (int64_t)sizeof(T));
@@ -311,29 +355,45 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         Reg::set(data[i], x);
       }
     }
-    // Rows past the chunk (and featureless lanes) read 0: make them -inf,
+    // Next ticket, while the loads are in flight. A workgroup that could
+    // wait for its segment takes it early only once every chunk of the
+    // segment has been handed out; otherwise after the wait. So a ticket
+    // held but not started never belongs to a segment its holder waits
+    // for, and waits only run down to chunks that are started.
+    if (t == 0 && early) next_s = (int64_t)taken;
+    // Rows past the item (and featureless lanes) read 0: make them -inf,
     // the identity of the max and a zero mass.
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       if (!(g.active && g.row_lane < rows - i * g.rows_step)) Reg::fill_neg_inf(data[i]);
     }
+    // Row groups wholly past the item (uniform) skip the arithmetic below.
+    auto live = [&](int i) { return i * g.rows_step < rows; };
     float m[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) m[v] = neg_inf();
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
+      if (!live(i)) continue;
 #pragma unroll
       for (int v = 0; v < VEC; ++v) m[v] = fmax_nan(m[v], Reg::get(data[i], v));
     }
     // Keep the rows packed across the reduction: without this the compiler
-    // keeps every unpacked f32 value alive until pass 2 (twice the registers,
-    // a quarter of the occupancy).
+    // keeps every unpacked f32 value alive until pass 2.
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
 #pragma unroll
       for (int w = 0; w < Reg::kCount; ++w) asm volatile("" : "+v"(data[i][w]));
     }
     block_allreduce<true, VEC>(m, g.lpr, g.feat_lane, lds);
+    if (tracing && t == 0) stamp_s[1] = wall_clock64();
+    // The reduction's barrier published next_s: prefetch the next item.
+    int64_t next = 0;
+    Item next_it;
+    if (early) {
+      next = next_s;
+      if (next < total) next_it = item_at(next);
+    }
     // 2. e = exp(x - m) in place, column sums. A column of only -inf has no
     //    mass: its reference is taken as 0 so that e = 0, not NaN.
     float ref[VEC], sum[VEC];
@@ -344,6 +404,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     }
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
+      if (!live(i)) continue;
       float e[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
@@ -357,73 +418,110 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       for (int w = 0; w < Reg::kCount; ++w) asm volatile("" : "+v"(data[i][w]));
     }
     block_allreduce<false, VEC>(sum, g.lpr, g.feat_lane, lds);
+    if (tracing && t == 0) stamp_s[2] = wall_clock64();
     // 3. Scale factor per column: exp(m - M) / S.
     float factor[VEC];
-    bool ready = true;
+    bool defer = false;
     if (!chunk) {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) factor[v] = fast_exp(m[v] - m[v]) / sum[v];
     } else {
-      if (g.row_lane == 0 && g.active) {
+      const int64_t idx = index_of(ticket);
+      const int64_t first = idx - it.c;
+      const int64_t parts = it.parts;
+      if (publisher) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          store_agent(p.partials + ticket * d + g.feature + v, m[v]);
-          store_agent(p.partial_sums + ticket * d + g.feature + v, sum[v]);
+        for (int v = 0; v < VEC; ++v) store_pair(p.pairs + idx * d + g.feature + v, m[v], sum[v]);
+      }
+      const bool direct = parts <= kDirect;
+      if (!direct) tree_merge(p, idx, first, parts, it.k, &flag_s);
+      if (!may_wait) {
+        defer = true;        // more chunks than the device surely holds at once
+      } else {
+        const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, lds, lds_s)
+                                  : wait_fold(p.final_pairs + it.k * d, 1, p.d, p.spin_ticks, lds, lds_s);
+        defer = !ready;
+        if (ready) {
+          __syncthreads();
+          if (g.active) {
+#pragma unroll
+            for (int v = 0; v < VEC; ++v) factor[v] = fast_exp(m[v] - lds[g.feature + v]) / lds_s[g.feature + v];
+          }
         }
       }
-      ready = merge_and_wait(p, ticket, k, first, parts, &flag_s);
-      if (ready && g.active) {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          const float big_m = load_agent(p.stats_max + k * d + g.feature + v);
-          const float big_s = load_agent(p.stats_sum + k * d + g.feature + v);
-          factor[v] = fast_exp(m[v] - big_m) / big_s;
-        }
-      }
-    }
-    if (!ready) {
-      if (t == 0) {
+      if (t == 0 && defer) {
         const int64_t slot = (int64_t)atomicAdd((unsigned long long*)(p.counters + 5), 1ull);
-        if (slot < p.items_cap) p.deferred[slot] = ticket;
+        if (slot < p.items_cap) p.deferred[slot] = idx;
       }
-      continue;
     }
-    // 4. Normalise from registers; rows past the chunk are dropped by the
-    //    resource's range check.
-    const Rsrc out = make_rsrc(static_cast<T*>(p.out) + start * d, chunk_elems * (int64_t)sizeof(T));
-    asm volatile("" : "+v"(voff));
+    if (t == 0 && !early) taken = atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+    if (tracing && t == 0) stamp_s[3] = wall_clock64();
+    if (!defer) {
+      // 4. Normalise from registers; rows past the item are dropped by the
+      //    resource's range check.
+      const Rsrc out = make_rsrc(static_cast<T*>(p.out) + start * d, chunk_elems * (int64_t)sizeof(T));
+      asm volatile("" : "+v"(voff));
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      float y[VEC];
+      for (int i = 0; i < RPT; ++i) {
+        if (!live(i)) continue;
+        float y[VEC];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) y[v] = Reg::get(data[i], v) * factor[v];
-      uint32_t w[In::kCount];
-      In::set(w, y);
-      buffer_store<In::kBytes>(out, voff + i * step_in, 0, w);
+        for (int v = 0; v < VEC; ++v) y[v] = Reg::get(data[i], v) * factor[v];
+        uint32_t w[In::kCount];
+        In::set(w, y);
+        buffer_store<In::kBytes>(out, voff + i * step_in, 0, w);
+      }
+      if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     }
-    if (p.visits && t == 0 && (!chunk || ticket == first)) atomicAdd(p.visits + s, 1);
+    if (!early) {
+      if (t == 0) next_s = (int64_t)taken;
+      __syncthreads();
+      next = next_s;
+      if (next < total) next_it = item_at(next);
+    }
+    if (tracing && t == 0) {
+      int64_t* r = p.trace + ticket * 8;
+      r[0] = ticket;
+      r[1] = stamp_s[0];
+      r[2] = stamp_s[1];
+      r[3] = stamp_s[2];
+      r[4] = stamp_s[3];
+      r[5] = wall_clock64();
+      r[6] = __smid();
+      r[7] = (chunk ? (it.parts <= kDirect ? 1 : 2) : 0) + (defer ? 4 : 0) + ((int64_t)rows << 8);
+    }
+    ticket = next;
+    it = next_it;
   }
 }
 
-// Chunks that gave up waiting: re-read and normalise with the segment's
-// published statistics (complete once k_softmax_fused has finished).
+// Chunks that did not normalise in k_softmax_fused (spin limit, or a segment
+// longer than the device holds at once): re-read and normalise with the
+// segment's merged statistics, complete once k_softmax_fused has finished.
 template <class T, class OffT, int VEC, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
   const int64_t count = p.counters[5] < p.items_cap ? p.counters[5] : p.items_cap;
   const int t = threadIdx.x;
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
+  __shared__ float lds_m[kBlock * VEC], lds_s[kBlock * VEC];
   for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
-    const int64_t item = p.deferred[i];
-    int64_t k, s, part, start, end;
-    item_rows<OffT>(p, item, k, s, part, start, end);
-    if (!g.active) continue;
-    float m[VEC], inv[VEC];
-    Elem<float>::load<VEC>(p.stats_max + k * p.d + g.feature, m);
-    Elem<float>::load<VEC>(p.stats_sum + k * p.d + g.feature, inv);
+    const int64_t slot = p.deferred[i];
+    const Item it = p.items[slot];
+    // Every pair is published once k_softmax_fused has finished.
+    if (it.parts <= kDirect) (void)fold_to_lds(p.pairs + (slot - it.c) * p.d, it.parts, p.d, lds_m, lds_s);
+    else (void)fold_to_lds(p.final_pairs + it.k * p.d, 1, p.d, lds_m, lds_s);
+    __syncthreads();
+    if (g.active) {
+      float m[VEC], inv[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) inv[v] = 1.0f / inv[v];
-    normalize_rows<T, VEC, MASK>(p, g, start, end, m, inv);
-    if (p.visits && t == 0 && part == 0) atomicAdd(p.visits + s, 1);
+      for (int v = 0; v < VEC; ++v) {
+        m[v] = lds_m[g.feature + v];
+        inv[v] = 1.0f / lds_s[g.feature + v];
+      }
+      normalize_rows<T, VEC, MASK>(p, g, it.start, it.start + it.rows, m, inv);
+    }
+    if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
+    __syncthreads();
   }
 }
 

@@ -507,11 +507,23 @@ __global__ __launch_bounds__(kBlock) void k_split_normalize(Params p) {
 #ifdef RG_PROLOGUE_KERNELS
 // Defined in exactly one translation unit (kernels_common.hip).
 
-// Zero the class counters (and the debug visit counts).
+// Zero the class counters (and the debug visit counts). For the
+// register-resident softmax also: every statistics pair slot gets the
+// unpublished sentinel and every merge counter 0 (grid-stride, coalesced).
 __global__ __launch_bounds__(kBlock) void k_init(Params p) {
-  if (threadIdx.x < 8) p.counters[threadIdx.x] = 0;
+  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t threads = (int64_t)gridDim.x * kBlock;
+  if (tid < 8) p.counters[tid] = 0;
   if (p.visits) {
-    for (int64_t s = threadIdx.x; s < p.b; s += kBlock) p.visits[s] = 0;
+    for (int64_t s = tid; s < p.b; s += threads) p.visits[s] = 0;
+  }
+  if (p.pairs) {
+    const uint64_t sentinel = (uint64_t)kSentinel << 32;
+    const int64_t slots = p.items_cap * p.d;
+    for (int64_t i = tid; i < slots; i += threads) p.pairs[i] = sentinel;
+    for (int64_t i = tid; i < p.b_split * p.d; i += threads) p.final_pairs[i] = sentinel;
+    for (int64_t i = tid; i < p.items_cap; i += threads) p.arrive[i] = 0;
+    for (int64_t i = tid; i < p.b_split; i += threads) p.seg_arrive[i] = 0;
   }
 }
 
@@ -524,9 +536,9 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
   const int64_t s = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
   const bool active = s < p.b;
-  int64_t length = 0;
+  int64_t length = 0, start = 0;
   if (active) {
-    int64_t start, end;
+    int64_t end;
     segment_rows<OffT>(p, s, start, end);
     length = end - start;
   }
@@ -543,21 +555,64 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
     base = __shfl(base, leader, kWave);
     const int64_t pos = base + __popcll(ballot & below);
     if (mine) p.queue[c * p.b + pos] = s;
+    // Register-resident softmax: whole segments of the wave and block
+    // classes are items too (wave class from the far end of the array).
+    if (mine && c < 2 && p.block_items)
+      p.block_items[c == 1 ? pos : p.b - 1 - pos] = Item{start, s, (int32_t)length, -1, 0, 1};
     if (c != 2) continue;
     // Split segments reserve ceil(L / part_rows) consecutive items. Valid
     // offsets never put more than b_split segments in the split queue;
-    // clamped invalid ones could, so never index past it.
+    // clamped invalid ones could, so never index past it. The
+    // register-resident softmax (p.items set) takes segments of more than
+    // kDirect chunks from the top of the item array, so they are dequeued
+    // first, while every workgroup of the grid is still free to hold one.
     long long first = 0, parts = 0;
+    bool fits = true;
     if (mine && pos < p.b_split) {
       parts = (length + p.part_rows - 1) / p.part_rows;
-      first = (long long)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
-      p.part_begin[pos] = first;
-      if (p.seg_arrive) {
-        p.seg_arrive[pos] = 0;
-        p.seg_ready[pos] = 0;
+      if (p.items && parts > kDirect) {
+        const long long above = (long long)atomicAdd((unsigned long long*)(p.counters + 6), (unsigned long long)parts);
+        first = (long long)p.items_cap - above - parts;
+        fits = first >= 0;
+      } else {
+        first = (long long)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
+        fits = first + parts <= p.items_cap;
       }
+      if (p.part_begin) p.part_begin[pos] = first;
     }
-    // The whole wave writes each split segment's item entries.
+    if (p.items) {
+      // Item descriptors. An allocation that does not fit the array (only
+      // inconsistent offsets make one) becomes empty items that touch no
+      // memory. Up to kDirect chunks: each lane writes its own segment's.
+      auto describe = [&](int64_t i, long long f, long long count, long long k, long long seg, long long seg_start,
+                          long long seg_rows, bool whole) {
+        const int64_t c = i - f;
+        const int64_t rows = seg_rows - c * p.part_rows < p.part_rows ? seg_rows - c * p.part_rows : p.part_rows;
+        Item item{0, seg, 0, -1, 1, 1};
+        if (whole) item = Item{seg_start + c * p.part_rows, seg, (int32_t)rows, (int32_t)k, (int32_t)c, (int32_t)count};
+        p.items[i] = item;
+      };
+      if (parts > 0 && parts <= kDirect) {
+        const int64_t lo = first > 0 ? first : 0;
+        const int64_t last = first + parts < p.items_cap ? first + parts : p.items_cap;
+        for (int64_t i = lo; i < last; ++i) describe(i, first, parts, pos, s, start, length, fits);
+      }
+      uint64_t todo = __ballot(parts > kDirect);
+      while (todo) {
+        const int src = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1;
+        const long long f = __shfl(first, src, kWave), count = __shfl(parts, src, kWave);
+        const int64_t lo = f > 0 ? f : 0;
+        const int64_t last = f + count < p.items_cap ? f + count : p.items_cap;
+        const long long k = __shfl((long long)pos, src, kWave), seg = __shfl((long long)s, src, kWave);
+        const long long seg_start = __shfl((long long)start, src, kWave);
+        const long long seg_rows = __shfl((long long)length, src, kWave);
+        const bool whole = __shfl((int)fits, src, kWave) != 0;
+        for (int64_t i = lo + lane; i < last; i += kWave) describe(i, f, count, k, seg, seg_start, seg_rows, whole);
+      }
+      continue;
+    }
+    // Split pipeline: the whole wave writes each split segment's entries.
     uint64_t todo = __ballot(parts > 0);
     while (todo) {
       const int src = __ffsll((unsigned long long)todo) - 1;
@@ -566,8 +621,7 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
       const long long k = __shfl((long long)pos, src, kWave);
       const int64_t last = f + count < p.items_cap ? f + count : p.items_cap;
       for (int64_t i = f + lane; i < last; i += kWave) {
-        p.item_pos[i] = k;
-        if (p.arrive) p.arrive[i] = 0;
+        if (p.item_pos) p.item_pos[i] = k;
       }
     }
   }

@@ -26,7 +26,8 @@ SCHEDULES = {"classified": 0, "naive": 1}
 ROLES = ("init", "classify", "wave", "block", "split_partial", "split_combine", "split_normalize", "naive",
          "fused", "deferred")
 BUFFERS = ("class_counts", "segment_ids", "item_segments", "part_begin", "partials", "partial_sums",
-           "max_stats", "sum_stats", "visits", "deferred", "arrive", "segment_arrive", "segment_ready")
+           "max_stats", "sum_stats", "visits", "deferred", "arrive", "segment_arrive", "items", "block_items",
+           "pairs", "final_pairs")
 MAX_LAUNCHES = 8
 
 RG_OK, RG_E_INVALID, RG_E_DEVICE, RG_E_UNSUPPORTED, RG_E_WORKSPACE = 0, -1, -2, -3, -4
@@ -88,6 +89,8 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         "rg_check_offsets": (c_int, [c_int, c_int, vp, c_i64, c_i64, c_i64, c_i64, vp, vp]),
         "rg_profile_start": (c_int, [vp, c_int]),
         "rg_module_set_spin_limit": (c_int, [vp, c_i64]),
+        "rg_module_set_trace": (c_int, [vp, vp, c_i64]),
+        "rg_device_clock_khz": (c_int, [c_int, ctypes.POINTER(c_i64)]),
         "rg_profile_stop": (c_int, [vp, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64),
                                     ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_i64)]),
     }
@@ -189,6 +192,11 @@ class NativeModule:
     def set_spin_limit(self, microseconds: int) -> None:
         """Bound of a softmax chunk's wait for its segment (test control)."""
         _check(library().rg_module_set_spin_limit(self._handle, microseconds), "rg_module_set_spin_limit")
+
+    def set_trace(self, buffer: int | None, records: int = 0) -> None:
+        """Item timeline of the register-resident softmax into ``buffer``
+        (device pointer to ``records`` x 8 int64), or off with None."""
+        _check(library().rg_module_set_trace(self._handle, buffer, records if buffer else 0), "rg_module_set_trace")
 
     def profile_start(self, max_calls: int) -> None:
         """Record per-launch HIP events in the next ``max_calls`` runs."""

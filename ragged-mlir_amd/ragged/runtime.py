@@ -313,7 +313,8 @@ class CompiledProgram:
                           "part_begin": torch.int64, "partials": torch.float32, "partial_sums": torch.float32,
                           "max_stats": torch.float32, "sum_stats": torch.float32, "visits": torch.int32,
                           "deferred": torch.int64, "arrive": torch.int32, "segment_arrive": torch.int32,
-                          "segment_ready": torch.int32}
+                          "items": torch.int64, "block_items": torch.int64, "pairs": torch.int64,
+                          "final_pairs": torch.int64}
                 for name, offset, nbytes in plan.buffers:
                     view = workspace[offset:offset + nbytes].view(dtypes[name])
                     if name == "segment_ids":

@@ -42,7 +42,7 @@ def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> 
         return [phase]
     roles = ["init", "classify"]
     if fused:
-        return roles + [f"wave_{phase}", "fused_online", "deferred_online"]
+        return roles + ["fused_online", "deferred_online"]
     for segment_class in classes:
         if segment_class == "split":
             roles += [f"split_partial_{phase}", f"split_combine_{phase}"]
@@ -60,21 +60,27 @@ def workspace_layout(spec: ProgramSpec, classified: bool, fused: bool = False) -
         return []
     d = spec.feature_dim
     workspace = [{"name": "class_counts", "dtype": "i64", "shape": [8]},
-                 {"name": "segment_ids", "dtype": "i64", "shape": [3, "B"]},
-                 {"name": "item_segments", "dtype": "i64", "shape": ["items"]},
-                 {"name": "part_begin", "dtype": "i64", "shape": ["B_split"]},
-                 {"name": "partials", "dtype": "f32", "shape": ["items", d]}]
+                 {"name": "segment_ids", "dtype": "i64", "shape": [3, "B"]}]
+    if fused:
+        workspace += [{"name": "deferred", "dtype": "i64", "shape": ["items"]},
+                      {"name": "arrive", "dtype": "i32", "shape": ["items"]},
+                      {"name": "segment_arrive", "dtype": "i32", "shape": ["B_split"]},
+                      {"name": "items", "dtype": "i64", "shape": ["items", 4]},
+                      {"name": "block_items", "dtype": "i64", "shape": ["B", 4]},
+                      {"name": "pairs", "dtype": "i64", "shape": ["items", d]},
+                      {"name": "final_pairs", "dtype": "i64", "shape": ["B_split", d]}]
+        if spec.debug_visits:
+            workspace.append({"name": "visits", "dtype": "i32", "shape": ["B"]})
+        return workspace
+    workspace += [{"name": "item_segments", "dtype": "i64", "shape": ["items"]},
+                  {"name": "part_begin", "dtype": "i64", "shape": ["B_split"]},
+                  {"name": "partials", "dtype": "f32", "shape": ["items", d]}]
     if spec.op == "softmax":
         workspace += [{"name": "partial_sums", "dtype": "f32", "shape": ["items", d]},
                       {"name": "max_stats", "dtype": "f32", "shape": ["B_split", d]},
                       {"name": "sum_stats", "dtype": "f32", "shape": ["B_split", d]}]
     if spec.debug_visits:
         workspace.append({"name": "visits", "dtype": "i32", "shape": ["B"]})
-    if fused:
-        workspace += [{"name": "deferred", "dtype": "i64", "shape": ["items"]},
-                      {"name": "arrive", "dtype": "i32", "shape": ["items"]},
-                      {"name": "segment_arrive", "dtype": "i32", "shape": ["B_split"]},
-                      {"name": "segment_ready", "dtype": "i32", "shape": ["B_split"]}]
     return workspace
 
 
