@@ -90,7 +90,7 @@ def oracle_gate(op, dtype, values_f32, offsets, out_device, torch, *, max_rows=6
     return stats
 
 
-def cpu_baseline(op, dtype, values_f32, offsets, *, target_seconds=8.0):
+def cpu_baseline(op, dtype, values_f32, offsets, *, target_seconds=15.0):
     """Time the NumPy oracle (single thread) on a prefix of segments that holds
     about 1/16 of the rows, scaled to µs per full call."""
     import oracle
@@ -111,13 +111,23 @@ def cpu_baseline(op, dtype, values_f32, offsets, *, target_seconds=8.0):
         function(inputs, sample_offsets)
         times.append(time.perf_counter() - t0)
     per_call_us = float(np.median(times)) * 1e6 * (n / max(rows, 1))
-    return {"value": round(per_call_us, 1), "unit": "µs/call", "cores": 1, "kind": "port",
-            "sample": f"float64 NumPy oracle ({op}) on the first {cut} of {len(lengths)} segments "
-                      f"({rows} of {n} rows), median of {len(times)} runs, scaled by N/rows"}
+    return {"per_call_us": round(per_call_us, 1), "cores": 1, "kind": "port",
+            "sample": f"float64 NumPy oracle ({op}, one thread) on the first {cut} of {len(lengths)} segments "
+                      f"({rows} of {n} rows), median of {len(times)} runs after one warm-up, scaled by N/rows"}
 
 
-def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_wave: int, t_block: int) -> int:
-    """Algorithmic bytes of the rows one kernel role owns."""
+def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_wave: int, t_block: int,
+               offset_bytes: int = 8) -> int:
+    """Algorithmic bytes of the rows one kernel role owns. The
+    register-resident softmax ("fused") reads every row once and writes every
+    row once: the whole call's value bytes. Its re-read pass ("deferred")
+    moves no algorithmic bytes; "classify" reads the offsets."""
+    if role == "fused":
+        return 2 * int(lengths.sum()) * d * element
+    if role == "classify":
+        return (len(lengths) + 1) * offset_bytes
+    if role in ("init", "deferred"):
+        return 0
     if role == "naive":
         rows = lengths
     elif role == "wave":
@@ -175,8 +185,14 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
             for _ in range(args.warmup):
                 program.run(x, off, out, select=select, max_len=max_len)
             torch.cuda.synchronize()
+            # The timed region: K calls bracketed by events on the current
+            # stream (the one the kernels run on), with the module recording
+            # a HIP event around every launch of those same calls.
+            chosen = program.naive if report.selected == "naive" else program
+            module = _modules[(0, chosen._digest)]
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             flush = torch.empty((1 << 30,), dtype=torch.uint8, device=device) if args.cold else None
+            module.profile_start(args.steps)
             if args.cold:
                 total_ms = 0.0
                 for _ in range(args.steps):
@@ -195,22 +211,14 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
                 end.record()
                 torch.cuda.synchronize()
                 ms = start.elapsed_time(end) / args.steps
-            # Per-kernel durations: events around every launch of K more calls.
-            chosen = program.naive if report.selected == "naive" else program
-            module = _modules[(0, chosen._digest)]
-            module.profile_start(args.steps)
-            for _ in range(args.steps):
-                if args.cold:
-                    flush.fill_(1)
-                program.run(x, off, out, select=select, max_len=max_len)
             profile = module.profile_stop()
-            torch.cuda.synchronize()
             plan = chosen._plans[(0, workload.n, workload.b)]
             total_bytes = algorithmic_bytes(op, workload.n, workload.b, workload.d, element, offset_bytes)
             kernels = {}
             for role, entry in profile["roles"].items():
                 avg = entry["ms"] / max(entry["launches"], 1)
-                nbytes = role_bytes(role, op, lengths, workload.d, element, int(plan.t_wave), int(plan.t_block))
+                nbytes = role_bytes(role, op, lengths, workload.d, element, int(plan.t_wave), int(plan.t_block),
+                                    offset_bytes)
                 kernels[role] = {"avg_ms": round(avg, 5), "bytes": nbytes,
                                  "gbps": round(nbytes / (avg * 1e-3) / 1e9, 1) if avg > 0 else None}
             dominant = max(kernels, key=lambda r: kernels[r]["avg_ms"]) if kernels else None
@@ -229,6 +237,40 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
     return results, workload
 
 
+def copy_probe(torch, mib: int, steps: int) -> int:
+    """A plain device-to-device copy of known size: under rocprofv3 --pmc its
+    FETCH_SIZE and WRITE_SIZE per dispatch give the counters' byte scale."""
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(7)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(max(steps, 1)):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / max(steps, 1)
+    print(json.dumps({"copy_bytes": n, "ms": round(ms, 4), "gbps": round(2 * n / (ms * 1e-3) / 1e9, 1)}), flush=True)
+    return 0
+
+
+def measured_traffic(workload: str, role: str | None):
+    """HBM bytes per launch of ``role``'s kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary of this workload, if it was measured with
+    the library that is loaded now (None otherwise)."""
+    path = ROOT / "profiles" / f"{role}_{workload}_traffic.json"
+    if not role or not path.exists():
+        return None
+    from ragged import native
+    data = json.loads(path.read_text())
+    if data.get("library_sha256") != native.library_sha256():
+        log(f"[bench] {path.name} was measured with another library build; traffic left null")
+        return None
+    return {"bytes": int(round(data["bytes"])), "source": f"profiles/{path.name}"}
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -239,6 +281,9 @@ def main(argv=None) -> int:
     parser.add_argument("--all", action="store_true", help="also measure forced classified and naive schedules")
     parser.add_argument("--details", type=Path, help="write every measured record as JSON to this file")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--copy-probe", type=int, metavar="MIB",
+                        help="instead: time a plain device copy of MIB MiB (--steps times), the known-size "
+                             "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = parser.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
@@ -248,6 +293,8 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 2
+    if args.copy_probe:
+        return copy_probe(torch, args.copy_probe, args.steps)
     from ragged import ArtifactCache
     with tempfile.TemporaryDirectory(prefix="ragged-bench-") as directory:
         cache = ArtifactCache(directory)
@@ -255,14 +302,18 @@ def main(argv=None) -> int:
         headline = next(r for r in records if r["select"] == "auto")
         baseline = None
         if not args.no_cpu:
-            baseline = cpu_baseline(headline["op"], workload.dtype, workload.values, workload.offsets)
-            baseline["cores"] = 1
+            sample = cpu_baseline(headline["op"], workload.dtype, workload.values, workload.offsets)
+            baseline = {"value": round(headline["algorithmic_bytes"] / (sample["per_call_us"] * 1e-6) / 1e9, 3),
+                        "unit": "GB/s", **sample}
             log(f"[bench] cpu baseline: {baseline}")
     dominant = headline["dominant"]
     kernel = headline["kernels"].get(dominant, {})
+    measured = measured_traffic(headline["workload"], dominant)
     roofline = {"bound": "hbm", "kernel": dominant, "achieved": kernel.get("gbps"), "peak": PEAK_GBPS,
                 "unit": "GB/s", "frac": round(kernel["gbps"] / PEAK_GBPS, 4) if kernel.get("gbps") else None,
-                "traffic": None, "avg_ms": kernel.get("avg_ms"), "bytes_per_launch": kernel.get("bytes"),
+                "traffic": measured.get("bytes") if measured else None,
+                "traffic_source": measured.get("source") if measured else None,
+                "avg_ms": kernel.get("avg_ms"), "bytes_per_launch": kernel.get("bytes"),
                 "call_gbps_gpu_time": round(headline["algorithmic_bytes"] / (headline["gpu_us_per_call"] * 1e-6) / 1e9, 1)}
     line = {
         "metric": METRIC, "value": headline["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

@@ -36,7 +36,7 @@ constexpr int kBlock = 256;            // threads of every workgroup-level worke
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kUnroll = 4;             // rows (or flat vectors) loaded per lane before folding
 constexpr int kCombineFeatures = 64;   // consecutive features per split-combine pass
-constexpr int kDirect = 8;             // register-resident softmax: chunks merged by all-read
+constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }

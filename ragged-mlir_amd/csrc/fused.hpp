@@ -47,6 +47,38 @@ constexpr int kRsrcWord3 = 0x00020000;   // raw 32-bit data format (gfx9 family)
 
 constexpr int kOutOfRange = 0x7ff00000;  // byte offset beyond any chunk resource
 
+// Item descriptors are read through the constant address space: they are
+// written by k_classify before this kernel starts and never during it, so
+// the loads go through the scalar cache into SGPRs (no VGPRs held while a
+// prefetch is in flight).
+typedef __attribute__((address_space(4))) const Item ConstItem;
+
+__device__ __forceinline__ Item load_item(ConstItem* item) {
+  Item it;
+  it.start = item->start;
+  it.seg = item->seg;
+  it.rows = item->rows;
+  it.k = item->k;
+  it.c = item->c;
+  it.parts = item->parts;
+  return it;
+}
+
+// A copy of a uniform flag the compiler cannot relate to other tests of the
+// same flag: stops it from duplicating the code between two such tests.
+__device__ __forceinline__ bool opaque(bool flag) {
+  int v = __builtin_amdgcn_readfirstlane((int)flag);
+  asm volatile("" : "+s"(v));
+  return v != 0;
+}
+
+// A workgroup-uniform 64-bit value (from LDS) in SGPRs.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ Rsrc make_rsrc(const void* base, int64_t bytes) {
   const int records = bytes > 0x7fffffff ? 0x7fffffff : (int)bytes;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, records, kRsrcWord3);
@@ -127,20 +159,38 @@ __device__ __forceinline__ void block_allreduce(float (&v)[VEC], int lpr, int fe
   }
   const int rep = lpr < kWave ? lpr : kWave;
   if (lane < rep) {
+    float* slot = lds + (w * kWave + lane) * VEC;
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) lds[(w * kWave + lane) * VEC + i] = v[i];
+    for (int i = 0; i < VEC; ++i) slot[i] = v[i];
   }
   __syncthreads();
-  // Waves holding feature lane fl: all four when lpr <= 64, else every
-  // (lpr/64)-th wave starting at fl/64.
-  const int stride = lpr <= kWave ? 1 : lpr / kWave;
-  const int w0 = lpr <= kWave ? 0 : feat_lane / kWave;
-  const int l0 = feat_lane & (kWave - 1);
+  if (lpr <= kWave) {
+    // Every wave holds every feature lane: fold waves 0..3 in order, at
+    // fixed offsets from one base address.
+    const float* base = lds + feat_lane * VEC;
 #pragma unroll
-  for (int i = 0; i < VEC; ++i) {
-    float acc = lds[(w0 * kWave + l0) * VEC + i];
-    for (int ww = w0 + stride; ww < kWavesPerBlock; ww += stride) acc = combine(acc, lds[(ww * kWave + l0) * VEC + i]);
-    v[i] = acc;
+    for (int i = 0; i < VEC; ++i) {
+      float acc = base[i];
+#pragma unroll
+      for (int ww = 1; ww < kWavesPerBlock; ++ww) acc = combine(acc, base[ww * kWave * VEC + i]);
+      v[i] = acc;
+    }
+  } else {
+    // A row spans lpr / 64 waves: feature lane fl lives in every
+    // (lpr/64)-th wave starting at fl / 64.
+    const int stride = lpr / kWave;
+    // Opaque: keeps the compiler from precomputing (and spilling) these
+    // addresses across the caller's loop for this rarely taken branch.
+    int offset = ((feat_lane / kWave) * kWave + (feat_lane & (kWave - 1))) * VEC;
+    asm volatile("" : "+v"(offset));
+    const float* base = lds + offset;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      float acc = base[i];
+      for (int ww = feat_lane / kWave + stride; ww < kWavesPerBlock; ww += stride)
+        acc = combine(acc, base[(ww - feat_lane / kWave) * kWave * VEC + i]);
+      v[i] = acc;
+    }
   }
   __syncthreads();
 }
@@ -170,23 +220,23 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F7
 
 // Segments of at most kDirect chunks merge directly: every chunk reads all
 // chunks' pairs. Longer ones fold groups of kGroup chunks (last arriver) and
-// then the groups (last group), and publish (M, S) in final_pairs. Every
-// fold spreads features over all threads and keeps kDirect independent
-// loads in flight per thread, so it costs ceil(count / kDirect) round trips.
+// then the groups (last group), and publish (M, S) in final_pairs; a
+// segment of one group publishes it from the group fold.
+constexpr int kBatch = 8;            // pair loads in flight per thread
 
-// Fold slots base[0], base[stride * d], ... (count of them) of feature f, in
-// slot order; *ready is false if any slot still holds the sentinel.
-__device__ __forceinline__ State<OP_SOFTMAX> fold_slots(const uint64_t* base, int64_t count, int64_t stride, int d,
-                                                        int64_t f, bool* ready) {
+// One thread's fold of slots base[0], base[stride * d], ... (count of them)
+// of feature f, in slot order, kBatch loads at a time; ok turns false if a
+// slot still holds the sentinel.
+__device__ __forceinline__ State<OP_SOFTMAX> fold_range(const uint64_t* base, int64_t count, int64_t stride, int d,
+                                                        int64_t f, bool& ok) {
   State<OP_SOFTMAX> acc;
   acc.init();
-  bool ok = true;
-  for (int64_t i0 = 0; i0 < count; i0 += kDirect) {
-    uint64_t v[kDirect];
+  for (int64_t i0 = 0; i0 < count; i0 += kBatch) {
+    uint64_t v[kBatch];
 #pragma unroll
-    for (int j = 0; j < kDirect; ++j) v[j] = i0 + j < count ? load_pair(base + (i0 + j) * stride * d + f) : 0;
+    for (int j = 0; j < kBatch; ++j) v[j] = i0 + j < count ? load_pair(base + (i0 + j) * stride * d + f) : 0;
 #pragma unroll
-    for (int j = 0; j < kDirect; ++j) {
+    for (int j = 0; j < kBatch; ++j) {
       if (i0 + j < count) {
         ok = ok && pair_ready(v[j]);
         State<OP_SOFTMAX> part;
@@ -196,41 +246,72 @@ __device__ __forceinline__ State<OP_SOFTMAX> fold_slots(const uint64_t* base, in
       }
     }
   }
-  *ready = ok;
   return acc;
 }
 
-// Whole workgroup: fold `count` consecutive slots of every feature into
-// (lds_m[f], lds_s[f]). True, after a barrier, when no slot held the sentinel.
-__device__ __forceinline__ bool fold_to_lds(const uint64_t* base, int64_t count, int d, float* lds_m, float* lds_s) {
+// Whole workgroup: fold `count` slots (stride apart) of every feature into
+// (lds_m[f], lds_s[f]). R threads per feature (the largest power of two with
+// R * d <= 256 and R <= count) fold R contiguous ranges of slots at once;
+// the R range results are folded in range order through `stage` (R * d
+// pairs). The association depends only on (count, d): deterministic. True,
+// after a barrier, when no slot held the sentinel.
+__device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, int64_t stride, int d, float* lds_m,
+                                           float* lds_s, uint64_t* stage) {
+  const int t = threadIdx.x;
+  int r = 1;
+  while (2 * r * d <= kBlock && 2 * r <= count) r *= 2;
   bool ok = true;
-  for (int f = threadIdx.x; f < d; f += kBlock) {
-    bool ready;
-    const State<OP_SOFTMAX> st = fold_slots(base, count, 1, d, f, &ready);
-    ok = ok && ready;
-    lds_m[f] = st.m;
-    lds_s[f] = st.s;
+  if (r == 1) {
+    for (int f = t; f < d; f += kBlock) {
+      const State<OP_SOFTMAX> st = fold_range(base, count, stride, d, f, ok);
+      lds_m[f] = st.m;
+      lds_s[f] = st.s;
+    }
+    return __syncthreads_or(!ok) == 0;
   }
-  return __syncthreads_or(!ok) == 0;
+  if (t < r * d) {
+    const int part = t / d, f = t - part * d;
+    const int64_t lo = count * part / r, hi = count * (part + 1) / r;
+    const State<OP_SOFTMAX> st = fold_range(base + lo * stride * d, hi - lo, stride, d, f, ok);
+    stage[t] = pack_pair(st.m, st.s);
+  }
+  const bool all = __syncthreads_or(!ok) == 0;
+  if (all && t < d) {
+    State<OP_SOFTMAX> acc;
+    acc.init();
+    for (int q = 0; q < r; ++q) {
+      State<OP_SOFTMAX> part;
+      part.m = pair_m(stage[q * d + t]);
+      part.s = pair_s(stage[q * d + t]);
+      acc.merge(part);
+    }
+    lds_m[t] = acc.m;
+    lds_s[t] = acc.s;
+  }
+  __syncthreads();
+  return all;
 }
 
-// fold_to_lds until every slot is published or the wall-clock budget ends
+// fold_block until every slot is published or the wall-clock budget ends
 // (the decision is thread 0's, so the workgroup agrees); false on timeout.
 __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, int d, int64_t spin_ticks,
-                                          float* lds_m, float* lds_s) {
+                                          float* lds_m, float* lds_s, uint64_t* stage) {
   const long long start = wall_clock64();
   for (;;) {
-    if (fold_to_lds(base, count, d, lds_m, lds_s)) return true;
+    if (fold_block(base, count, 1, d, lds_m, lds_s, stage)) return true;
     if (__syncthreads_or(threadIdx.x == 0 && wall_clock64() - start >= spin_ticks)) return false;
     __builtin_amdgcn_s_sleep(2);
   }
 }
 
 // Counter-based tree merge of a long segment: the last chunk of each group
-// folds the group into slot gfirst, the last group folds the groups into
-// final_pairs[k]. Never waits.
-__device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t k, int* flag_s) {
+// folds the group into slot gfirst (into final_pairs[k] when the segment is
+// one group), the last group folds the groups into final_pairs[k]. Never
+// waits.
+__device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t k, int* flag_s,
+                           float* lds_m, float* lds_s, uint64_t* stage) {
   const int t = threadIdx.x;
+  const int d = p.d;
   const int64_t group = (slot - first) / kGroup;
   const int64_t gfirst = first + group * kGroup;
   const int64_t gsize = parts - group * kGroup < kGroup ? parts - group * kGroup : kGroup;
@@ -243,11 +324,10 @@ __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t
   const bool last_in_group = *flag_s != 0;
   __syncthreads();
   if (!last_in_group) return;
-  for (int f = t; f < p.d; f += kBlock) {
-    bool ready;
-    const State<OP_SOFTMAX> g = fold_slots(p.pairs + gfirst * p.d, gsize, 1, p.d, f, &ready);
-    store_pair(p.pairs + gfirst * p.d + f, g.m, g.s);
-  }
+  (void)fold_block(p.pairs + gfirst * d, gsize, 1, d, lds_m, lds_s, stage);
+  uint64_t* dest = groups == 1 ? p.final_pairs + k * d : p.pairs + gfirst * d;
+  for (int f = t; f < d; f += kBlock) store_pair(dest + f, lds_m[f], lds_s[f]);
+  if (groups == 1) return;
   wait_stores();
   __syncthreads();
   if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == groups - 1;
@@ -255,11 +335,8 @@ __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t
   const bool last_group = *flag_s != 0;
   __syncthreads();
   if (!last_group) return;
-  for (int f = t; f < p.d; f += kBlock) {
-    bool ready;
-    const State<OP_SOFTMAX> g = fold_slots(p.pairs + first * p.d, groups, kGroup, p.d, f, &ready);
-    store_pair(p.final_pairs + k * p.d + f, g.m, g.s);
-  }
+  (void)fold_block(p.pairs + first * d, groups, kGroup, d, lds_m, lds_s, stage);
+  for (int f = t; f < d; f += kBlock) store_pair(p.final_pairs + k * d + f, lds_m[f], lds_s[f]);
 }
 
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
@@ -272,6 +349,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   // lds: reductions, then the segment's merged max per feature; lds_s: its sum.
   __shared__ float lds[kBlock * VEC];
   __shared__ float lds_s[kBlock * VEC];
+  __shared__ uint64_t stage[kBlock];    // partial folds of the segment merge
+  __shared__ float own_m[kBlock * VEC];   // this item's column max and sum
+  __shared__ float own_s[kBlock * VEC];
   __shared__ int64_t next_s;
   __shared__ int flag_s;
   __shared__ int64_t stamp_s[5];    // item timeline (diagnostics), thread 0 only
@@ -292,19 +372,20 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   const int step_in = g.rows_step * p.d * (int)sizeof(T);
   const int voff_mask = g.active ? (g.row_lane * p.d + g.feature) * 4 : kOutOfRange;
   const int step_mask = g.rows_step * p.d * 4;
-  const bool publisher = g.row_lane == 0 && g.active;   // one thread per feature group
   // Index of a chunk ticket in the item (and pair) arrays.
   auto index_of = [&](int64_t ticket) -> int64_t {
     return ticket < n_tree ? p.items_cap - n_tree + ticket : ticket - n_tree;
   };
+  ConstItem* items = (ConstItem*)p.items;
+  ConstItem* block_items = (ConstItem*)p.block_items;
   auto item_at = [&](int64_t ticket) -> Item {
-    if (ticket < n_split) return p.items[index_of(ticket)];
-    if (ticket < n_split + n_block) return p.block_items[ticket - n_split];
-    return p.block_items[p.b - 1 - (ticket - n_split - n_block)];
+    if (ticket < n_split) return load_item(items + index_of(ticket));
+    if (ticket < n_split + n_block) return load_item(block_items + (ticket - n_split));
+    return load_item(block_items + (p.b - 1 - (ticket - n_split - n_block)));
   };
   if (t == 0) next_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
   __syncthreads();
-  int64_t ticket = next_s;
+  int64_t ticket = uniform64(next_s);
   Item it;
   if (ticket < total) it = item_at(ticket);
   while (ticket < total) {
@@ -319,8 +400,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     __syncthreads();
     unsigned long long taken = 0;
     if (t == 0 && early) taken = atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
-    const bool tracing = p.trace && ticket < p.trace_cap;
-    if (tracing && t == 0) stamp_s[0] = wall_clock64();
+    // Timeline stamps are unconditional (cheap); only the record is optional.
+    if (t == 0) stamp_s[0] = wall_clock64();
     const int rows = it.rows;
     const int64_t start = it.start;
     const int64_t chunk_elems = (int64_t)rows * d;
@@ -360,7 +441,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     // segment has been handed out; otherwise after the wait. So a ticket
     // held but not started never belongs to a segment its holder waits
     // for, and waits only run down to chunks that are started.
-    if (t == 0 && early) next_s = (int64_t)taken;
+    if (t == 0 && opaque(early)) next_s = (int64_t)taken;
     // Rows past the item (and featureless lanes) read 0: make them -inf,
     // the identity of the max and a zero mass.
 #pragma unroll
@@ -368,13 +449,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       if (!(g.active && g.row_lane < rows - i * g.rows_step)) Reg::fill_neg_inf(data[i]);
     }
     // Row groups wholly past the item (uniform) skip the arithmetic below.
-    auto live = [&](int i) { return i * g.rows_step < rows; };
+    auto live = [&](int i) { return i == 0 || i * g.rows_step < rows; };
     float m[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) m[v] = neg_inf();
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      if (!live(i)) continue;
 #pragma unroll
       for (int v = 0; v < VEC; ++v) m[v] = fmax_nan(m[v], Reg::get(data[i], v));
     }
@@ -386,12 +466,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       for (int w = 0; w < Reg::kCount; ++w) asm volatile("" : "+v"(data[i][w]));
     }
     block_allreduce<true, VEC>(m, g.lpr, g.feat_lane, lds);
-    if (tracing && t == 0) stamp_s[1] = wall_clock64();
+    if (t == 0) stamp_s[1] = wall_clock64();
     // The reduction's barrier published next_s: prefetch the next item.
     int64_t next = 0;
     Item next_it;
-    if (early) {
-      next = next_s;
+    if (opaque(early)) {
+      next = uniform64(next_s);
       if (next < total) next_it = item_at(next);
     }
     // 2. e = exp(x - m) in place, column sums. A column of only -inf has no
@@ -418,35 +498,37 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       for (int w = 0; w < Reg::kCount; ++w) asm volatile("" : "+v"(data[i][w]));
     }
     block_allreduce<false, VEC>(sum, g.lpr, g.feat_lane, lds);
-    if (tracing && t == 0) stamp_s[2] = wall_clock64();
-    // 3. Scale factor per column: exp(m - M) / S.
-    float factor[VEC];
+    if (t == 0) stamp_s[2] = wall_clock64();
+    // The item's column statistics leave registers for LDS: the merge below
+    // then holds nothing but the rows.
+    if (g.row_lane == 0 && g.active) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        own_m[g.feature + v] = m[v];
+        own_s[g.feature + v] = sum[v];
+      }
+    }
+    __syncthreads();
+    // 3. Scale factor per column, into lds[f]: exp(m - M) / S.
     bool defer = false;
     if (!chunk) {
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) factor[v] = fast_exp(m[v] - m[v]) / sum[v];
+      for (int f = t; f < d; f += kBlock) lds[f] = fast_exp(own_m[f] - own_m[f]) / own_s[f];
     } else {
       const int64_t idx = index_of(ticket);
       const int64_t first = idx - it.c;
       const int64_t parts = it.parts;
-      if (publisher) {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) store_pair(p.pairs + idx * d + g.feature + v, m[v], sum[v]);
-      }
+      for (int f = t; f < d; f += kBlock) store_pair(p.pairs + idx * d + f, own_m[f], own_s[f]);
       const bool direct = parts <= kDirect;
-      if (!direct) tree_merge(p, idx, first, parts, it.k, &flag_s);
+      if (!direct) tree_merge(p, idx, first, parts, it.k, &flag_s, lds, lds_s, stage);
       if (!may_wait) {
         defer = true;        // more chunks than the device surely holds at once
       } else {
-        const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, lds, lds_s)
-                                  : wait_fold(p.final_pairs + it.k * d, 1, p.d, p.spin_ticks, lds, lds_s);
+        const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, lds, lds_s, stage)
+                                  : wait_fold(p.final_pairs + it.k * d, 1, p.d, p.spin_ticks, lds, lds_s, stage);
         defer = !ready;
+        // Same thread wrote lds[f] / lds_s[f] in the fold: no barrier needed.
         if (ready) {
-          __syncthreads();
-          if (g.active) {
-#pragma unroll
-            for (int v = 0; v < VEC; ++v) factor[v] = fast_exp(m[v] - lds[g.feature + v]) / lds_s[g.feature + v];
-          }
+          for (int f = t; f < d; f += kBlock) lds[f] = fast_exp(own_m[f] - lds[f]) / lds_s[f];
         }
       }
       if (t == 0 && defer) {
@@ -454,13 +536,17 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         if (slot < p.items_cap) p.deferred[slot] = idx;
       }
     }
-    if (t == 0 && !early) taken = atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
-    if (tracing && t == 0) stamp_s[3] = wall_clock64();
+    __syncthreads();
+    if (t == 0 && !opaque(early)) taken = atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+    if (t == 0) stamp_s[3] = wall_clock64();
     if (!defer) {
       // 4. Normalise from registers; rows past the item are dropped by the
       //    resource's range check.
       const Rsrc out = make_rsrc(static_cast<T*>(p.out) + start * d, chunk_elems * (int64_t)sizeof(T));
       asm volatile("" : "+v"(voff));
+      float factor[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) factor[v] = g.active ? lds[g.feature + v] : 0.f;
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         if (!live(i)) continue;
@@ -473,13 +559,13 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       }
       if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     }
-    if (!early) {
+    if (!opaque(early)) {
       if (t == 0) next_s = (int64_t)taken;
       __syncthreads();
-      next = next_s;
+      next = uniform64(next_s);
       if (next < total) next_it = item_at(next);
     }
-    if (tracing && t == 0) {
+    if (opaque(p.trace && ticket < p.trace_cap) && t == 0) {
       int64_t* r = p.trace + ticket * 8;
       r[0] = ticket;
       r[1] = stamp_s[0];
@@ -488,7 +574,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       r[4] = stamp_s[3];
       r[5] = wall_clock64();
       r[6] = __smid();
-      r[7] = (chunk ? (it.parts <= kDirect ? 1 : 2) : 0) + (defer ? 4 : 0) + ((int64_t)rows << 8);
+      r[7] = (opaque(chunk) ? (it.parts <= kDirect ? 1 : 2) : 0) + (defer ? 4 : 0) + ((int64_t)rows << 8);
     }
     ticket = next;
     it = next_it;
@@ -504,12 +590,13 @@ __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
   const int t = threadIdx.x;
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
   __shared__ float lds_m[kBlock * VEC], lds_s[kBlock * VEC];
+  __shared__ uint64_t stage[kBlock];
   for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
     const int64_t slot = p.deferred[i];
     const Item it = p.items[slot];
     // Every pair is published once k_softmax_fused has finished.
-    if (it.parts <= kDirect) (void)fold_to_lds(p.pairs + (slot - it.c) * p.d, it.parts, p.d, lds_m, lds_s);
-    else (void)fold_to_lds(p.final_pairs + it.k * p.d, 1, p.d, lds_m, lds_s);
+    if (it.parts <= kDirect) (void)fold_block(p.pairs + (slot - it.c) * p.d, it.parts, 1, p.d, lds_m, lds_s, stage);
+    else (void)fold_block(p.final_pairs + it.k * p.d, 1, 1, p.d, lds_m, lds_s, stage);
     __syncthreads();
     if (g.active) {
       float m[VEC], inv[VEC];

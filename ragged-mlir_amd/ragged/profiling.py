@@ -1,0 +1,175 @@
+"""rocprofv3 summaries: per-kernel durations and HBM traffic counters.
+
+The analogue of the reference's ``bench/profile.py:120-144`` (which
+summarises Nsight Compute metrics) for rocprofv3 output on gfx950:
+
+* ``stats``: rocprofv3 ``--kernel-trace --stats`` output reduced to calls /
+  average / total per kernel;
+* ``counters``: ``rocprofv3 --pmc X`` output reduced to the mean value per
+  dispatch of counter X for each kernel, summing the rows one dispatch
+  reports (one per TCC channel on some ROCm versions);
+* ``traffic``: FETCH_SIZE and WRITE_SIZE runs of a workload, each scaled by
+  the factor the same counter reads for a plain copy of known size
+  (``bench.py --copy-probe``), into HBM bytes per launch.
+
+Both output formats are read: the SQLite database rocprofv3 writes by
+default (``*_results.db``, views ``kernels`` and ``counters_collection``) and
+``--output-format csv`` files (``*_kernel_stats.csv``,
+``*_counter_collection.csv``). No GPU and no torch, so it also runs as a
+script: ``python ragged-mlir_amd/ragged/profiling.py traffic ...``.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+from pathlib import Path
+import re
+import sqlite3
+import sys
+from typing import Iterable
+
+
+def _rows(path: Path) -> list[dict[str, str]]:
+    with open(path, newline="", encoding="utf-8") as handle:
+        return list(csv.DictReader(handle))
+
+
+def _column(row: dict[str, str], *names: str) -> str:
+    for name in names:
+        if name in row:
+            return row[name]
+    raise KeyError(f"none of {names} in columns {sorted(row)}")
+
+
+def short_name(kernel: str) -> str:
+    """``rg::k_softmax_fused<__bf16, long, 8, 16, false, false>(rg::Params)``
+    -> ``k_softmax_fused<__bf16, long, 8, 16, false, false>``."""
+    name = re.sub(r"\(.*\)$", "", kernel.strip())
+    name = re.sub(r"^void\s+", "", name)
+    return name.split("::", 1)[-1] if name.startswith("rg::") else name
+
+
+def _query(path: Path, sql: str) -> list[tuple]:
+    connection = sqlite3.connect(f"file:{path}?mode=ro", uri=True)
+    try:
+        return connection.execute(sql).fetchall()
+    finally:
+        connection.close()
+
+
+def kernel_stats(path: Path) -> dict[str, dict[str, float]]:
+    """Per kernel: calls, average and total ns, share of the total."""
+    out: dict[str, dict[str, float]] = {}
+    if Path(path).suffix == ".db":
+        records = [(short_name(name), 1, float(duration))
+                   for name, duration in _query(path, "select name, duration from kernels")]
+    else:
+        records = [(short_name(_column(row, "Name", "KernelName", "Kernel_Name")), int(_column(row, "Calls")),
+                    float(_column(row, "TotalDurationNs", "Total_Duration_Ns"))) for row in _rows(path)]
+    for name, calls, total in records:
+        entry = out.setdefault(name, {"calls": 0, "total_ns": 0.0})
+        entry["calls"] += calls
+        entry["total_ns"] += total
+    grand = sum(e["total_ns"] for e in out.values()) or 1.0
+    for entry in out.values():
+        entry["avg_ns"] = entry["total_ns"] / max(entry["calls"], 1)
+        entry["pct"] = 100.0 * entry["total_ns"] / grand
+    return out
+
+
+def counter_per_dispatch(path: Path, counter: str) -> dict[str, dict[str, float]]:
+    """Per kernel: dispatches and mean value of ``counter`` per dispatch."""
+    per_dispatch: dict[tuple[str, str], float] = {}
+    if Path(path).suffix == ".db":
+        records = [(str(dispatch), short_name(name), float(value)) for dispatch, name, value in
+                   _query(path, "select dispatch_id, kernel_name, value from counters_collection "
+                                f"where counter_name = '{counter}'")]
+    else:
+        records = [(_column(row, "Dispatch_Id", "Dispatch-Id"), short_name(_column(row, "Kernel_Name", "Kernel-Name")),
+                    float(_column(row, "Counter_Value", "Counter-Value"))) for row in _rows(path)
+                   if _column(row, "Counter_Name", "Counter-Name") == counter]
+    for dispatch, name, value in records:
+        key = (dispatch, name)
+        per_dispatch[key] = per_dispatch.get(key, 0.0) + value
+    out: dict[str, dict[str, float]] = {}
+    for (_, name), value in per_dispatch.items():
+        entry = out.setdefault(name, {"dispatches": 0, "sum": 0.0})
+        entry["dispatches"] += 1
+        entry["sum"] += value
+    for entry in out.values():
+        entry["mean"] = entry["sum"] / entry["dispatches"]
+    return out
+
+
+def _match(table: dict[str, dict[str, float]], pattern: str) -> tuple[str, dict[str, float]]:
+    hits = [(name, entry) for name, entry in table.items() if re.search(pattern, name)]
+    if not hits:
+        raise KeyError(f"no kernel matches {pattern!r}; kernels: {sorted(table)}")
+    return max(hits, key=lambda item: item[1].get("total_ns", item[1].get("sum", 0.0)))
+
+
+def copy_factor(fetch_csv: Path, write_csv: Path, copy_bytes: int, pattern: str) -> dict[str, float]:
+    """Bytes per counter unit for FETCH_SIZE and WRITE_SIZE, from a copy that
+    reads and writes ``copy_bytes`` per dispatch."""
+    _, fetch = _match(counter_per_dispatch(fetch_csv, "FETCH_SIZE"), pattern)
+    _, write = _match(counter_per_dispatch(write_csv, "WRITE_SIZE"), pattern)
+    return {"fetch_bytes_per_unit": copy_bytes / fetch["mean"], "write_bytes_per_unit": copy_bytes / write["mean"],
+            "copy_bytes": copy_bytes, "fetch_units": fetch["mean"], "write_units": write["mean"]}
+
+
+def traffic(fetch_csv: Path, write_csv: Path, pattern: str, factor: dict[str, float]) -> dict[str, float]:
+    """HBM bytes per launch of the kernel matching ``pattern``."""
+    name, fetch = _match(counter_per_dispatch(fetch_csv, "FETCH_SIZE"), pattern)
+    _, write = _match(counter_per_dispatch(write_csv, "WRITE_SIZE"), pattern)
+    read_bytes = fetch["mean"] * factor["fetch_bytes_per_unit"]
+    write_bytes = write["mean"] * factor["write_bytes_per_unit"]
+    return {"kernel": name, "dispatches": fetch["dispatches"], "fetch_units": fetch["mean"],
+            "write_units": write["mean"], "read_bytes": read_bytes, "write_bytes": write_bytes,
+            "bytes": read_bytes + write_bytes}
+
+
+def stats_table(stats: dict[str, dict[str, float]], limit: int = 12) -> Iterable[str]:
+    yield "| kernel | calls | avg µs | total µs | % |"
+    yield "|---|---:|---:|---:|---:|"
+    for name, entry in sorted(stats.items(), key=lambda item: -item[1]["total_ns"])[:limit]:
+        yield (f"| `{name}` | {entry['calls']} | {entry['avg_ns'] / 1e3:.2f} | {entry['total_ns'] / 1e3:.1f} | "
+               f"{entry['pct']:.1f} |")
+
+
+def main(argv: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = parser.add_subparsers(dest="command", required=True)
+    s = sub.add_parser("stats", help="per-kernel table of a *_kernel_stats.csv")
+    s.add_argument("csv", type=Path)
+    s.add_argument("--json", action="store_true")
+    c = sub.add_parser("counters", help="mean per dispatch of one counter")
+    c.add_argument("csv", type=Path)
+    c.add_argument("counter")
+    t = sub.add_parser("traffic", help="HBM bytes per launch from FETCH_SIZE / WRITE_SIZE runs")
+    t.add_argument("--fetch", type=Path, required=True)
+    t.add_argument("--write", type=Path, required=True)
+    t.add_argument("--kernel", required=True, help="regex of the kernel name")
+    t.add_argument("--copy-fetch", type=Path, required=True)
+    t.add_argument("--copy-write", type=Path, required=True)
+    t.add_argument("--copy-bytes", type=int, required=True)
+    t.add_argument("--copy-kernel", default="copy|elementwise", help="regex of the copy kernel")
+    t.add_argument("--algorithmic-bytes", type=int, help="per launch, for the ratio")
+    args = parser.parse_args(argv)
+    if args.command == "stats":
+        table = kernel_stats(args.csv)
+        print(json.dumps(table, indent=1) if args.json else "\n".join(stats_table(table)))
+    elif args.command == "counters":
+        print(json.dumps(counter_per_dispatch(args.csv, args.counter), indent=1))
+    else:
+        factor = copy_factor(args.copy_fetch, args.copy_write, args.copy_bytes, args.copy_kernel)
+        result = {"factor": factor, **traffic(args.fetch, args.write, args.kernel, factor)}
+        if args.algorithmic_bytes:
+            result["algorithmic_bytes"] = args.algorithmic_bytes
+            result["traffic_over_algorithmic"] = result["bytes"] / args.algorithmic_bytes
+        print(json.dumps(result, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
