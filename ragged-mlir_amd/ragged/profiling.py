@@ -155,6 +155,9 @@ def main(argv: list[str] | None = None) -> int:
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--copy-kernel", default="copy|elementwise", help="regex of the copy kernel")
     t.add_argument("--algorithmic-bytes", type=int, help="per launch, for the ratio")
+    t.add_argument("--library", type=Path, help="the libragged_hip.so that was profiled (its sha256 is recorded)")
+    t.add_argument("--command", action="append", default=[], help="a command that produced the inputs (repeat)")
+    t.add_argument("--out", type=Path, help="also write the result as JSON here")
     args = parser.parse_args(argv)
     if args.command == "stats":
         table = kernel_stats(args.csv)
@@ -167,7 +170,15 @@ def main(argv: list[str] | None = None) -> int:
         if args.algorithmic_bytes:
             result["algorithmic_bytes"] = args.algorithmic_bytes
             result["traffic_over_algorithmic"] = result["bytes"] / args.algorithmic_bytes
-        print(json.dumps(result, indent=1))
+        if args.library:
+            import hashlib
+            result["library_sha256"] = hashlib.sha256(args.library.read_bytes()).hexdigest()
+        if args.command:
+            result["commands"] = args.command
+        text = json.dumps(result, indent=1)
+        if args.out:
+            args.out.write_text(text + "\n")
+        print(text)
     return 0
 
 

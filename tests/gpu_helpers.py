@@ -53,9 +53,15 @@ def check(actual: np.ndarray, values: np.ndarray, offsets: np.ndarray, *, op: st
     if mask is not None or scale != 1.0:
         logits = oracle.masked_logits(inputs, mask if mask is not None else np.zeros_like(inputs), scale=scale)
         if op == "softmax":
+            oracle.assert_matches(actual, logits, offsets, operation=op, input_dtype=dtype,
+                                  tolerances=oracle.STRICT_TOLERANCES)
             return oracle.assert_matches(actual, logits, offsets, operation=op, input_dtype=dtype)
         inputs = logits
     stats = oracle.assert_matches(actual, inputs, offsets, operation=op, input_dtype=dtype)
+    # The build's own bar: rtol 1e-5 (f32) / 1e-2 (bf16) for sum and softmax,
+    # with the reference's absolute floor (oracle.STRICT_TOLERANCES).
+    oracle.assert_matches(actual, inputs, offsets, operation=op, input_dtype=dtype,
+                          tolerances=oracle.STRICT_TOLERANCES)
     if op == "max":
         expected = oracle.segment_max(inputs, offsets).astype(np.float32)
         if dtype == "bf16":

@@ -1,0 +1,160 @@
+"""CPU tests of the host layer: the C-ABI library's exported symbols and
+host-only entry points, the restated input generators against the
+reference's recorded hashes, spec validation, checked-mode status decoding,
+the cost model's features, and the loud failure when the HIP library is
+missing. No test here launches a kernel."""
+from __future__ import annotations
+
+import ctypes
+import json
+from pathlib import Path
+import re
+
+import numpy as np
+import pytest
+
+
+from ragged import ProgramSpec
+from ragged import native
+from ragged.errors import RuntimeUnavailable, ValidationError
+from ragged.selection import features
+from ragged.validation import CONDITIONS, I64_MAX, raise_for_status
+from ragged.workloads import describe, make_lengths, offsets_from_lengths, reference_values, sha256
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "ragged_hip.h"
+GOLDEN = REPO / "tests" / "golden" / "reference_cases.json"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(rg_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = declared_functions()
+    for required in ("rg_abi_version", "rg_last_error", "rg_device_query", "rg_module_create", "rg_plan_create",
+                     "rg_run", "rg_check_offsets", "rg_module_resident"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = native.library()
+    missing = [name for name in declared_functions() if not hasattr(lib, name)]
+    assert not missing, f"declared in {HEADER.name} but not exported: {missing}"
+
+
+def test_abi_version_and_build_info():
+    lib = native.library()
+    version = int(re.search(r"#define\s+RG_ABI_VERSION\s+(\d+)", HEADER.read_text()).group(1))
+    assert lib.rg_abi_version() == version == native.ABI_VERSION
+    info = lib.rg_build_info().decode()
+    assert "target=gfx950" in info and "packed-fp32-ops" in info
+
+
+@pytest.mark.parametrize("dtype,d,capacity", [("bf16", 128, 256), ("f32", 128, 128), ("bf16", 64, 512),
+                                              ("f32", 1024, 16)])
+def test_register_resident_defaults(dtype, d, capacity):
+    """Softmax specs whose rows fit one workgroup's registers default to the
+    register-resident schedule, with one chunk = the workgroup's capacity."""
+    spec = native.make_spec("softmax", dtype, "i64", d)
+    assert native.uses_fused(spec)
+    assert spec.part_rows == capacity and spec.t_block == capacity and spec.t_wave == 0
+
+
+def test_reductions_keep_the_class_pipeline():
+    for op in ("sum", "max"):
+        spec = native.make_spec(op, "f32", "i64", 128)
+        assert not native.uses_fused(spec)
+        assert 0 < spec.t_wave < spec.t_block and spec.part_rows > 0
+
+
+def test_spec_defaults_rejects_bad_input():
+    lib = native.library()
+    spec = native.Spec(9, 0, 1, 128, 1.0, 0, 1, 0, -1, -1, -1)
+    assert lib.rg_module_create(0, ctypes.byref(spec), ctypes.byref(ctypes.c_void_p())) != 0
+    assert lib.rg_last_error()
+
+
+def test_generators_match_reference_hashes():
+    """Every recorded reference benchmark input (lengths, offsets and, for
+    the smaller cases, values) regenerates bit-identically."""
+    cases = json.loads(GOLDEN.read_text())["cases"]
+    assert len(cases) >= 100
+    values_checked = 0
+    for case in cases:
+        lengths = make_lengths(case["distribution"], case["segments"], seed=case["seed"],
+                               total_elements=case["total_elements"], mean_length=case["mean_length"])
+        stats = describe(lengths)
+        assert stats["lengths_sha256"] == case["lengths_sha256"], case["source"]
+        assert stats["histogram_counts"] == case["histogram_counts"]
+        assert stats["max_length"] == case["max_length"]
+        assert sha256(offsets_from_lengths(lengths, case["offsets_dtype"])) == case["offsets_sha256"]
+        if case["elements"] * case["d"] <= 1 << 20:
+            values = reference_values(case["seed"], case["elements"], case["d"])
+            assert sha256(values) == case["values_sha256"], case["source"]
+            values_checked += 1
+    assert values_checked >= 20
+
+
+@pytest.mark.parametrize("kwargs,message", [
+    ({"op": "mean"}, "op must be"),
+    ({"op": "sum", "dtype": "f16"}, "dtype"),
+    ({"op": "sum", "feature_dim": 0}, "feature_dim"),
+    ({"op": "sum", "feature_dim": 1025}, "feature_dim"),
+    ({"op": "sum", "offsets_dtype": "u64"}, "offsets_dtype"),
+    ({"op": "sum", "mask": True}, "mask"),
+    ({"op": "max", "alias": "inplace"}, "in-place"),
+    ({"op": "softmax", "scale": float("inf")}, "scale"),
+])
+def test_program_spec_validation(kwargs, message):
+    with pytest.raises(ValidationError, match=message):
+        ProgramSpec(**kwargs)
+
+
+def test_spec_identity_is_stable():
+    a = ProgramSpec("softmax", "bf16", 128, "i64")
+    b = ProgramSpec("softmax", "bf16", 128, "i64")
+    c = ProgramSpec("softmax", "bf16", 64, "i64")
+    assert a.ir_hash == b.ir_hash != c.ir_hash
+    assert ProgramSpec.from_dict(a.to_dict()) == a
+
+
+def test_status_decoding_known_answers():
+    clean = [I64_MAX] * 7
+    raise_for_status(clean, b=4)
+    status = list(clean)
+    status[CONDITIONS.index("nonmonotone")] = 2
+    status[CONDITIONS.index("above_n")] = 3
+    with pytest.raises(ValidationError) as info:
+        raise_for_status(status, b=4)
+    assert info.value.errors == {"above_n": 3, "nonmonotone": 2}
+    bad = list(clean)
+    bad[0] = 1                     # first_nonzero can only be reported at index 0
+    with pytest.raises(ValidationError, match="domain"):
+        raise_for_status(bad, b=4)
+    with pytest.raises(ValidationError, match="layout"):
+        raise_for_status(clean[:6], b=4)
+
+
+def test_cost_model_features_known_answer():
+    # N = 2^20 rows, B = 1024, D = 4 f32, L = 2^14: M = 16, S = 2^14*4*4/2^20 = 0.25 MiB,
+    # skew = 2^14*1024/2^20 = 16 -> M*log2(skew) = 64; working set (N + B rows) = 16.015625 MiB,
+    # under the 32 MiB L2.
+    assert features(2**20, 1024, 4, 2**14, 4, "sum") == (1.0, 16.0, 0.25, 1.024, 64.0, 0.0, 0.0)
+    # Softmax writes N rows: 128 MiB of rows at D=32 f32 -> 256 MiB working set.
+    f = features(2**20, 1024, 32, 2**14, 4, "softmax")
+    assert f[5] == pytest.approx(256.0 - 32.0) and f[6] == 0.0
+
+
+def test_product_fails_loudly_without_the_library(monkeypatch, tmp_path):
+    monkeypatch.setattr(native, "LIBRARY_PATH", tmp_path / "missing.so")
+    with pytest.raises(RuntimeUnavailable, match="missing"):
+        native.library_sha256()
+
+
+def test_oracle_is_test_infrastructure_only():
+    """Nothing in the product package imports the oracle."""
+    for path in (REPO / "ragged-mlir_amd" / "ragged").glob("*.py"):
+        text = path.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), path.name

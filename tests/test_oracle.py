@@ -309,3 +309,20 @@ def test_oracle_does_not_import_product_or_torch():
             else:
                 continue
             assert all(name.split(".")[0] not in {"ragged", "torch", "triton"} for name in names)
+
+
+def test_strict_tolerance_table_is_tighter_and_rejects_what_it_should():
+    """The build's bar (rtol 1e-5 f32, 1e-2 bf16) accepts a 5e-6 relative
+    error on f32 and rejects 1.5e-5, which the reference's 2e-5 accepts."""
+    values = np.array([[1.0], [2.0], [3.0]], dtype=np.float32)
+    offsets = np.array([0, 3], dtype=np.int64)
+    for dtype in ("f32", "bf16"):
+        assert oracle.STRICT_TOLERANCES[dtype][0] < oracle.TOLERANCES[dtype][0]
+    ok = np.array([[6.0 * (1 + 5e-6)]])
+    oracle.assert_matches(ok, values, offsets, operation="sum", input_dtype="f32",
+                          tolerances=oracle.STRICT_TOLERANCES)
+    off = np.array([[6.0 * (1 + 1.5e-5)]])
+    oracle.assert_matches(off, values, offsets, operation="sum", input_dtype="f32")
+    with pytest.raises(AssertionError):
+        oracle.assert_matches(off, values, offsets, operation="sum", input_dtype="f32",
+                              tolerances=oracle.STRICT_TOLERANCES)
