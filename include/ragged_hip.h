@@ -192,6 +192,8 @@ int rg_module_set_spin_limit(rg_module* module, int64_t microseconds);
  * rows << 8). A null buffer turns it off. No counterpart in the reference:
  * a measurement hook only. */
 int rg_module_set_trace(rg_module* module, void* buffer, int64_t records);
+
+/* Rate of the device wall clock the timeline records use, in kHz. */
 int rg_device_clock_khz(int device, int64_t* khz);
 
 /* Measurement: while profiling is on, rg_run records a HIP event before
