@@ -128,6 +128,13 @@ def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_
         return (len(lengths) + 1) * offset_bytes
     if role in ("init", "deferred"):
         return 0
+    if role == "worker":
+        # The classified worker reads every row once; it writes every
+        # reduction result, or the softmax rows of unsplit segments (split
+        # segments' rows are written by split_normalize).
+        if op == "softmax":
+            return (int(lengths.sum()) + int(lengths[lengths <= t_block].sum())) * d * element
+        return (int(lengths.sum()) + len(lengths)) * d * element
     if role == "naive":
         rows = lengths
     elif role == "wave":
@@ -186,33 +193,44 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
                 program.run(x, off, out, select=select, max_len=max_len)
             torch.cuda.synchronize()
             # The timed region: K calls bracketed by events on the current
-            # stream (the one the kernels run on), with the module recording
-            # a HIP event around every launch of those same calls.
+            # stream (the one the kernels run on). A second pass of K calls
+            # records a HIP event around every launch (per-kernel times);
+            # those events add gaps between launches, so that pass is not
+            # the per-call figure.
             chosen = program.naive if report.selected == "naive" else program
             module = _modules[(0, chosen._digest)]
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             flush = torch.empty((1 << 30,), dtype=torch.uint8, device=device) if args.cold else None
-            module.profile_start(args.steps)
-            if args.cold:
-                total_ms = 0.0
-                for _ in range(args.steps):
-                    flush.fill_(1)
-                    start.record()
-                    program.run(x, off, out, select=select, max_len=max_len)
-                    end.record()
-                    torch.cuda.synchronize()
-                    total_ms += start.elapsed_time(end)
-                ms = total_ms / args.steps
-            else:
+
+            def timed_calls() -> float:
+                if args.cold:
+                    total_ms = 0.0
+                    for _ in range(args.steps):
+                        flush.fill_(1)
+                        start.record()
+                        program.run(x, off, out, select=select, max_len=max_len)
+                        end.record()
+                        torch.cuda.synchronize()
+                        total_ms += start.elapsed_time(end)
+                    return total_ms / args.steps
                 torch.cuda.synchronize()
+                host = []
                 start.record()
                 for _ in range(args.steps):
+                    t_host = time.perf_counter()
                     program.run(x, off, out, select=select, max_len=max_len)
+                    host.append((time.perf_counter() - t_host) * 1e6)
                 end.record()
                 torch.cuda.synchronize()
-                ms = start.elapsed_time(end) / args.steps
+                host_us.append([round(float(np.median(host)), 1), round(float(np.max(host)), 1)])
+                return start.elapsed_time(end) / args.steps
+
+            host_us = []     # [median, max] host time of one run() call per timed pass
+            ms = timed_calls()
+            module.profile_start(args.steps)
+            timed_calls()
             profile = module.profile_stop()
-            plan = chosen._plans[(0, workload.n, workload.b)]
+            plan = next(v for k, v in chosen._plans.items() if k[:3] == (0, workload.n, workload.b))
             total_bytes = algorithmic_bytes(op, workload.n, workload.b, workload.d, element, offset_bytes)
             kernels = {}
             for role, entry in profile["roles"].items():
@@ -227,11 +245,13 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
             results.append({
                 "workload": workload.name, "op": op, "select": select, "selected": report.selected,
                 "us_per_call": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
-                "gpu_us_per_call": round(gpu_ms * 1e3, 2), "algorithmic_bytes": total_bytes, "kernels": kernels,
+                "gpu_us_per_call": round(gpu_ms * 1e3, 2), "host_us_per_run": host_us[0] if host_us else None,
+                "algorithmic_bytes": total_bytes, "kernels": kernels,
                 "dominant": dominant, "cold": bool(args.cold), "oracle": stats,
                 "n": workload.n, "b": workload.b, "d": workload.d, "dtype": workload.dtype,
                 "offsets_dtype": workload.offsets_dtype, "max_len": workload.max_len,
                 "kernel_names": list(report.kernel_names), "grids": [list(g) for g in report.grids]})
+            log(f"[bench] {workload.name} {op} {select}: host run() median/max us {host_us[0] if host_us else None}")
             log(f"[bench] {workload.name} {op} {select}: {ms * 1e3:.1f} us/call, {gbps:.0f} GB/s "
                 f"({100 * gbps / PEAK_GBPS:.1f}% of peak); kernels {json.dumps(kernels)}")
     return results, workload

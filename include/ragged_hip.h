@@ -41,21 +41,27 @@ enum rg_status {
 enum rg_op { RG_OP_SUM = 0, RG_OP_MAX = 1, RG_OP_SOFTMAX = 2 };
 enum rg_dtype { RG_F32 = 0, RG_BF16 = 1 };
 enum rg_index { RG_I32 = 0, RG_I64 = 1 };
-enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1 };
+/* RG_SHORT_SEGMENTS: every segment is expected to be at most t_wave rows
+ * (the caller's max_len says so): one worker launch takes the segments in
+ * order, with no classification and no workspace. Any input is still
+ * computed exactly; a longer segment only runs slower. Not available for the
+ * register-resident softmax (its t_wave is 0). */
+enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1, RG_SHORT_SEGMENTS = 2 };
 
 /* Kernel roles, in launch order of the classified schedule. */
 enum rg_role {
   RG_ROLE_INIT = 0,
   RG_ROLE_CLASSIFY = 1,
-  RG_ROLE_WAVE = 2,            /* wave64 worker: one wave per short segment */
-  RG_ROLE_BLOCK = 3,           /* workgroup worker: one 256-thread group per segment */
-  RG_ROLE_SPLIT_PARTIAL = 4,   /* one workgroup per part of a long segment */
-  RG_ROLE_SPLIT_COMBINE = 5,   /* fold the parts of each long segment */
+  RG_ROLE_WAVE = 2,            /* not launched: the wave class runs inside RG_ROLE_WORKER */
+  RG_ROLE_BLOCK = 3,           /* not launched: the block class runs inside RG_ROLE_WORKER */
+  RG_ROLE_SPLIT_PARTIAL = 4,   /* not launched: split parts run inside RG_ROLE_WORKER */
+  RG_ROLE_SPLIT_COMBINE = 5,   /* not launched: the last part of a segment combines, inside RG_ROLE_WORKER */
   RG_ROLE_SPLIT_NORMALIZE = 6, /* softmax: normalise each part */
   RG_ROLE_NAIVE = 7,           /* block-per-segment schedule */
   RG_ROLE_FUSED = 8,           /* softmax: register-resident worker over all block/split items */
   RG_ROLE_DEFERRED = 9,        /* softmax: re-read pass for chunks that stopped waiting */
-  RG_ROLE_COUNT = 10
+  RG_ROLE_WORKER = 10,         /* persistent worker over the wave, block and split queues */
+  RG_ROLE_COUNT = 11
 };
 
 #define RG_MAX_LAUNCHES 8
@@ -124,7 +130,7 @@ enum rg_buffer {
   RG_BUF_VISITS = 8,        /* i32[B] (debug_visits) */
   RG_BUF_DEFERRED = 9,      /* i64[items_cap] chunks left to the re-read pass (fused softmax) */
   RG_BUF_ARRIVE = 10,       /* i32[items_cap] chunk arrivals per 32-chunk group (fused softmax) */
-  RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] group arrivals per split segment (fused softmax) */
+  RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] part (fused softmax: group) arrivals per split segment */
   RG_BUF_ITEMS = 12,        /* 32-byte descriptors [items_cap] of split chunks (fused softmax) */
   RG_BUF_BLOCK_ITEMS = 13,  /* 32-byte descriptors [B] of whole segments (fused softmax) */
   RG_BUF_PAIRS = 14,        /* u64[items_cap, D] published (max, sum) of each chunk (fused softmax) */

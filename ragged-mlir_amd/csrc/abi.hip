@@ -48,8 +48,8 @@ constexpr int64_t kGridMax = 2147483647;
 // Class boundaries and part size in bytes of segment data; row thresholds
 // follow from the row size (see rg_spec_defaults).
 constexpr int64_t kWaveBytes = 8 << 10;     // one wave64 reads up to 8 KiB
-constexpr int64_t kBlockBytes = 128 << 10;  // one workgroup reads up to 128 KiB
-constexpr int64_t kPartBytes = 64 << 10;    // a split part is 64 KiB of rows
+constexpr int64_t kBlockBytes = 512 << 10;  // one workgroup reads up to 512 KiB
+constexpr int64_t kPartBytes = 256 << 10;   // a split part is 256 KiB of rows
 
 int element_bytes(int dtype) { return dtype == RG_BF16 ? 2 : 4; }
 
@@ -170,10 +170,14 @@ int rg_spec_defaults(rg_spec* spec) {
   if (spec->dtype != RG_F32 && spec->dtype != RG_BF16) return fail(RG_E_INVALID, "dtype must be f32 or bf16");
   const int64_t row = (int64_t)spec->feature_dim * element_bytes(spec->dtype);
   const bool default_wave = spec->t_wave < 0;
-  if (default_wave) spec->t_wave = std::max<int64_t>(1, kWaveBytes / row);
+  const Geometry geo = choose_geometry(spec->dtype, spec->feature_dim, spec->vectorize != 0);
+  // Wave class: in the flat mapping (D below the vector width) the segments
+  // one lane reduces on its own, else what one wave reads in one pass.
+  if (default_wave)
+    spec->t_wave = geo.flat ? std::max<int64_t>(1, rg::kLaneElems / spec->feature_dim)
+                            : std::max<int64_t>(1, kWaveBytes / row);
   // Softmax with a register-resident worker: a block-class segment and a
   // split chunk are exactly what one workgroup holds in registers.
-  const Geometry geo = choose_geometry(spec->dtype, spec->feature_dim, spec->vectorize != 0);
   const int64_t capacity = spec->op == RG_OP_SOFTMAX
       ? fused_capacity(spec->dtype, spec->feature_dim, geo.vec, geo.flat,
                        spec->has_mask != 0 || spec->scale != 1.0f)
@@ -241,10 +245,7 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
   }
   module->roles[RG_ROLE_INIT] = rg::kernel_init();
   module->roles[RG_ROLE_CLASSIFY] = rg::kernel_classify(spec.offsets_dtype);
-  module->roles[RG_ROLE_WAVE] = k.wave;
-  module->roles[RG_ROLE_BLOCK] = k.block;
-  module->roles[RG_ROLE_SPLIT_PARTIAL] = k.split_partial;
-  module->roles[RG_ROLE_SPLIT_COMBINE] = k.split_combine;
+  module->roles[RG_ROLE_WORKER] = k.worker;
   module->roles[RG_ROLE_SPLIT_NORMALIZE] = k.split_normalize;
   module->roles[RG_ROLE_NAIVE] = k.naive;
   const bool f32_logits = spec.has_mask != 0 || spec.scale != 1.0f;
@@ -374,7 +375,10 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   if (!module || !plan) return fail(RG_E_INVALID, "rg_plan_create: null argument");
   if (n < 0 || b < 0) return fail(RG_E_INVALID, "N and B must be nonnegative");
   if (b == 0 && n != 0) return fail(RG_E_INVALID, "B=0 requires N=0");
-  if (schedule != RG_CLASSIFIED && schedule != RG_BLOCK_PER_SEGMENT) return fail(RG_E_INVALID, "unknown schedule");
+  if (schedule != RG_CLASSIFIED && schedule != RG_BLOCK_PER_SEGMENT && schedule != RG_SHORT_SEGMENTS)
+    return fail(RG_E_INVALID, "unknown schedule");
+  if (schedule == RG_SHORT_SEGMENTS && (module->fused || module->spec.t_wave < 1))
+    return fail(RG_E_INVALID, "this specialisation has no short-segment schedule");
   if (schedule == RG_BLOCK_PER_SEGMENT && module->spec.debug_visits)
     return fail(RG_E_INVALID, "debug visits require the classified schedule");
   const rg_spec& spec = module->spec;
@@ -409,6 +413,12 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     add_launch(RG_ROLE_NAIVE, b, tiles_block);
     return RG_OK;
   }
+  if (schedule == RG_SHORT_SEGMENTS) {
+    // Batches of segments in order, grid-stride: no counters, no workspace.
+    const int64_t batch = geo.flat ? rg::kBlock : rg::kWavesPerBlock;
+    add_launch(RG_ROLE_WORKER, std::min(module->resident[RG_ROLE_WORKER], (b + batch - 1) / batch), 1);
+    return RG_OK;
+  }
 
   // Workspace: every buffer at a 256-byte aligned offset of one allocation.
   const int64_t b_split = std::min<int64_t>(b, n / (spec.t_block + 1));
@@ -427,6 +437,8 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     return fail(RG_E_INVALID, "split workspace bytes overflow");
   sizes[RG_BUF_COUNTERS] = 8 * 8;
   if (!module->fused) {
+    // Part arrivals per split segment (the worker's last part combines).
+    if (!mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE])) return fail(RG_E_INVALID, "arrival bytes overflow");
     sizes[RG_BUF_PARTIALS] = item_bytes;
     if (softmax) {
       sizes[RG_BUF_PARTIAL_SUMS] = item_bytes;
@@ -466,25 +478,15 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     if (b_split) add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], items_cap), 1);
     return RG_OK;
   }
-  const int64_t wave_groups = (b + rg::kWavesPerBlock - 1) / rg::kWavesPerBlock;
-  add_launch(RG_ROLE_WAVE, std::min(module->resident[RG_ROLE_WAVE] / std::max<int64_t>(tiles_wave, 1), wave_groups),
-             tiles_wave);
-  add_launch(RG_ROLE_BLOCK, std::min(module->resident[RG_ROLE_BLOCK] / std::max<int64_t>(tiles_block, 1), b),
-             tiles_block);
-  if (b_split) {
-    add_launch(RG_ROLE_SPLIT_PARTIAL,
-               std::min(module->resident[RG_ROLE_SPLIT_PARTIAL] / std::max<int64_t>(tiles_block, 1), items_cap),
+  // One persistent worker drains the wave, block and split queues (as many
+  // workgroups as are resident, fewer when there is less work: a ticket is
+  // a split part, a block segment or a batch of wave segments).
+  const int64_t tickets = items_cap * tiles_block + b;
+  add_launch(RG_ROLE_WORKER, std::min(module->resident[RG_ROLE_WORKER], std::max<int64_t>(tickets, 1)), 1);
+  if (b_split && softmax)
+    add_launch(RG_ROLE_SPLIT_NORMALIZE,
+               std::min(module->resident[RG_ROLE_SPLIT_NORMALIZE] / std::max<int64_t>(tiles_block, 1), items_cap),
                tiles_block);
-    const int64_t ft = combine_features_host(d);
-    const int64_t tiles_combine = (d + ft - 1) / ft;
-    add_launch(RG_ROLE_SPLIT_COMBINE,
-               std::min(module->resident[RG_ROLE_SPLIT_COMBINE] / std::max<int64_t>(tiles_combine, 1), b_split),
-               tiles_combine);
-    if (softmax)
-      add_launch(RG_ROLE_SPLIT_NORMALIZE,
-                 std::min(module->resident[RG_ROLE_SPLIT_NORMALIZE] / std::max<int64_t>(tiles_block, 1), items_cap),
-                 tiles_block);
-  }
   return RG_OK;
 }
 
@@ -522,6 +524,7 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
   auto buffer = [&](int index) -> void* {
     return plan->buffer_bytes[index] ? base + plan->buffer_offset[index] : nullptr;
   };
+  p.short_segments = plan->schedule == RG_SHORT_SEGMENTS ? 1 : 0;
   if (plan->schedule == RG_CLASSIFIED) {
     p.counters = static_cast<int64_t*>(buffer(RG_BUF_COUNTERS));
     p.queue = static_cast<int64_t*>(buffer(RG_BUF_QUEUE));

@@ -36,6 +36,7 @@ constexpr int kBlock = 256;            // threads of every workgroup-level worke
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kUnroll = 4;             // rows (or flat vectors) loaded per lane before folding
 constexpr int kCombineFeatures = 64;   // consecutive features per split-combine pass
+constexpr int kLaneElems = 256;        // classified worker: flat elements one lane reduces alone
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
@@ -95,6 +96,7 @@ struct Params {
   int64_t trace_cap;
   int64_t* status;         // [7] checked-offsets status
   int64_t min_len, max_len;  // checked-offsets hints, -1 when absent
+  int32_t short_segments;  // worker: every segment in order as wave class (no queues)
 };
 
 // ---------------------------------------------------------------------------

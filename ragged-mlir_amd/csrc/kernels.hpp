@@ -5,11 +5,11 @@
 //    workgroup each (reference: the direct schedule, ToGPU.cpp:1283-1349).
 //  * classified: k_init + k_classify bin every segment by length into a
 //    wave64 queue, a workgroup queue and a split queue (reference:
-//    ToGPU.cpp:901-998, with wave64 thresholds); persistent workers drain
-//    each queue (ToGPU.cpp:999-1045). A split segment is cut into
-//    ceil(L / part_rows) parts -- proportional to its length instead of the
-//    reference's fixed 8 -- each processed by one workgroup; k_split_combine
-//    folds the parts (ToGPU.cpp:399-472) and, for softmax,
+//    ToGPU.cpp:901-998, with wave64 thresholds); one persistent worker
+//    (worker.hpp) drains the queues (ToGPU.cpp:999-1045). A split segment is
+//    cut into ceil(L / part_rows) parts -- proportional to its length instead
+//    of the reference's fixed 8 -- each processed by one workgroup; the last
+//    part folds them (ToGPU.cpp:399-472) and, for softmax,
 //    k_split_normalize writes the probabilities (ToGPU.cpp:279-281).
 #pragma once
 
@@ -333,32 +333,6 @@ __global__ __launch_bounds__(kBlock) void k_naive(Params p) {
   }
 }
 
-// Wave-class worker: every wave drains queue 0 independently.
-template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_wave(Params p) {
-  const int64_t count = p.counters[0];
-  const int64_t stride = (int64_t)gridDim.x * kWavesPerBlock;
-  for (int64_t pos = (int64_t)blockIdx.x * kWavesPerBlock + threadIdx.x / kWave; pos < count; pos += stride) {
-    const int64_t s = p.queue[pos];
-    int64_t start, end;
-    segment_rows<OffT>(p, s, start, end);
-    process_segment<OP, T, VEC, FLAT, MASK, false>(p, s, start, end, blockIdx.y, nullptr);
-  }
-}
-
-// Block-class worker: every workgroup drains queue 1.
-template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_block(Params p) {
-  __shared__ float lds[kBlock * VEC * 2];
-  const int64_t count = p.counters[1];
-  for (int64_t pos = blockIdx.x; pos < count; pos += gridDim.x) {
-    const int64_t s = p.queue[p.b + pos];
-    int64_t start, end;
-    segment_rows<OffT>(p, s, start, end);
-    process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, blockIdx.y, lds);
-  }
-}
-
 // Rows of split item `item`: its part of its segment.
 template <class OffT>
 __device__ __forceinline__ void item_rows(const Params& p, int64_t item, int64_t& k, int64_t& s, int64_t& part,
@@ -373,103 +347,12 @@ __device__ __forceinline__ void item_rows(const Params& p, int64_t item, int64_t
   end = start + p.part_rows > seg_end ? seg_end : start + p.part_rows;
 }
 
-// One part of a split segment -> partials[item, :] (and partial_sums).
-template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_split_partial(Params p) {
-  __shared__ float lds[kBlock * VEC * 2];
-  const int64_t items = p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap;
-  const int t = threadIdx.x;
-  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    int64_t k, s, part, start, end;
-    item_rows<OffT>(p, item, k, s, part, start, end);
-    State<OP> st[VEC];
-    init_all<OP, VEC>(st);
-    if constexpr (FLAT) {
-      fold_flat<OP, T, VEC, MASK>(p, kBlock, t, start * p.d, end * p.d, st);
-      merge_components<OP, VEC>(st, p.d);
-      block_reduce<OP, VEC>(st, 1, 0, lds);
-      if (t == 0) {
-        for (int f = 0; f < p.d; ++f) {
-          if constexpr (OP == OP_SUM) p.partials[item * p.d + f] = st[f].s;
-          else p.partials[item * p.d + f] = st[f].m;
-          if constexpr (OP == OP_SOFTMAX) p.partial_sums[item * p.d + f] = st[f].s;
-        }
-      }
-    } else {
-      const RowGeo g = row_geo<VEC>(p.d, kBlock, t, blockIdx.y);
-      fold_rows<OP, T, VEC, MASK>(p, g, start, end, st);
-      block_reduce<OP, VEC>(st, g.lpr, g.feat_lane, lds);
-      if (g.row_lane == 0 && g.active) {
-        float x[VEC];
-        result_of<OP, VEC>(st, x);
-        Elem<float>::store<VEC>(p.partials + item * p.d + g.feature, x);
-        if constexpr (OP == OP_SOFTMAX) {
-          float y[VEC];
-#pragma unroll
-          for (int v = 0; v < VEC; ++v) y[v] = st[v].s;
-          Elem<float>::store<VEC>(p.partial_sums + item * p.d + g.feature, y);
-        }
-      }
-    }
-  }
-}
-
-// Fold the parts of each split segment. Threads = part lanes x feature lanes
-// (kCombineFeatures consecutive features, coalesced); LDS tree over part lanes.
+// Features folded at once when a split segment's parts are combined:
+// threads = part lanes x feature lanes (consecutive features, coalesced).
 __device__ __forceinline__ int combine_features(int d) {
   int f = 1;
   while (f < d && f < kCombineFeatures) f <<= 1;
   return f;
-}
-
-template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_split_combine(Params p) {
-  __shared__ float lds[kBlock * 2];
-  constexpr int S = Slots<OP>::kCount;
-  const int ft = combine_features(p.d);
-  const int pl_count = kBlock / ft;
-  const int fl = threadIdx.x % ft, pl = threadIdx.x / ft;
-  const int64_t f = (int64_t)blockIdx.y * ft + fl;
-  const int64_t count = p.counters[2] < p.b_split ? p.counters[2] : p.b_split;
-  for (int64_t k = blockIdx.x; k < count; k += gridDim.x) {
-    const int64_t s = p.queue[2 * p.b + k];
-    int64_t start, end;
-    segment_rows<OffT>(p, s, start, end);
-    const int64_t parts = (end - start + p.part_rows - 1) / p.part_rows;
-    int64_t first = p.part_begin[k];
-    int64_t last = first + parts < p.items_cap ? first + parts : p.items_cap;
-    State<OP> acc;
-    acc.init();
-    if (f < p.d) {
-      for (int64_t item = first + pl; item < last; item += pl_count) {
-        if constexpr (OP == OP_SUM) {
-          acc.fold(p.partials[item * p.d + f]);
-        } else {
-          State<OP> part;
-          part.m = p.partials[item * p.d + f];
-          if constexpr (OP == OP_SOFTMAX) part.s = p.partial_sums[item * p.d + f];
-          acc.merge(part);
-        }
-      }
-    }
-    st_write<OP>(lds + threadIdx.x, kBlock, acc);
-    __syncthreads();
-    if (pl == 0) {
-      for (int q = 1; q < pl_count; ++q) acc.merge(st_read<OP>(lds + q * ft + fl, kBlock));
-      if (f < p.d) {
-        if constexpr (OP == OP_SOFTMAX) {
-          p.stats_max[k * p.d + f] = acc.m;
-          p.stats_sum[k * p.d + f] = acc.s;
-        } else {
-          Elem<T>::put(static_cast<T*>(p.out) + s * p.d + f, value_of<OP>(acc));
-        }
-      }
-      if constexpr (OP != OP_SOFTMAX) {
-        if (p.visits && blockIdx.y == 0 && threadIdx.x == 0) atomicAdd(p.visits + s, 1);
-      }
-    }
-    __syncthreads();
-  }
 }
 
 // Softmax normalisation of each split part with the combined statistics.
@@ -517,13 +400,15 @@ __global__ __launch_bounds__(kBlock) void k_init(Params p) {
   if (p.visits) {
     for (int64_t s = tid; s < p.b; s += threads) p.visits[s] = 0;
   }
+  if (p.seg_arrive) {
+    for (int64_t i = tid; i < p.b_split; i += threads) p.seg_arrive[i] = 0;
+  }
   if (p.pairs) {
     const uint64_t sentinel = (uint64_t)kSentinel << 32;
     const int64_t slots = p.items_cap * p.d;
     for (int64_t i = tid; i < slots; i += threads) p.pairs[i] = sentinel;
     for (int64_t i = tid; i < p.b_split * p.d; i += threads) p.final_pairs[i] = sentinel;
     for (int64_t i = tid; i < p.items_cap; i += threads) p.arrive[i] = 0;
-    for (int64_t i = tid; i < p.b_split; i += threads) p.seg_arrive[i] = 0;
   }
 }
 
@@ -544,16 +429,39 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
   }
   const int cls = length <= p.t_wave ? 0 : (length <= p.t_block ? 1 : 2);
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  // Queue runs: the workgroup reserves each class's run with one atomic
+  // (not one per wave: every wave of the grid adding to the same three
+  // counters serialises at the memory side), and each wave takes its part
+  // of the run in wave order, so a wave's (and the workgroup's) segments of
+  // one class sit in consecutive positions in segment order
+  // (classified-abi.md:56-66).
+  __shared__ long long run_s[3][kWavesPerBlock];
+  const int wave = threadIdx.x / kWave;
+  uint64_t ballots[3];
+#pragma unroll
+  for (int c = 0; c < 3; ++c) {
+    ballots[c] = __ballot(active && cls == c);
+    if (lane == 0) run_s[c][wave] = (long long)__popcll(ballots[c]);
+  }
+  __syncthreads();
+  if (threadIdx.x < 3) {
+    const int c = threadIdx.x;
+    long long total = 0;
+    for (int w = 0; w < kWavesPerBlock; ++w) total += run_s[c][w];
+    long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + c), (unsigned long long)total) : 0;
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      const long long count = run_s[c][w];
+      run_s[c][w] = base;
+      base += count;
+    }
+  }
+  __syncthreads();
 #pragma unroll
   for (int c = 0; c < 3; ++c) {
     const bool mine = active && cls == c;
-    const uint64_t ballot = __ballot(mine);
+    const uint64_t ballot = ballots[c];
     if (ballot == 0) continue;
-    const int leader = __ffsll((unsigned long long)ballot) - 1;
-    long long base = 0;
-    if (lane == leader) base = (long long)atomicAdd((unsigned long long*)(p.counters + c), (unsigned long long)__popcll(ballot));
-    base = __shfl(base, leader, kWave);
-    const int64_t pos = base + __popcll(ballot & below);
+    const int64_t pos = run_s[c][wave] + __popcll(ballot & below);
     if (mine) p.queue[c * p.b + pos] = s;
     // Register-resident softmax: whole segments of the wave and block
     // classes are items too (wave class from the far end of the array).

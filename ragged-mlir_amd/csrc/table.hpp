@@ -8,15 +8,13 @@
 #include <type_traits>
 
 #include "fused.hpp"
+#include "worker.hpp"
 
 namespace rg {
 
 struct KernelSet {
   const void* naive;
-  const void* wave;
-  const void* block;
-  const void* split_partial;
-  const void* split_combine;
+  const void* worker;            // classified schedule: wave, block and split classes in one launch
   const void* split_normalize;   // softmax only
   const void* fused;             // softmax, row mapping: register-resident worker
   const void* fused_f32;         // same, storing f32 logits (scale or mask on bf16 input)
@@ -75,10 +73,7 @@ const void* kernel_offsets_check(int offsets_dtype);
 
 #define RG_SET(OP, T, OFFT, VEC, FLAT, MASK)                                              \
   {(const void*)&rg::k_naive<OP, T, OFFT, VEC, FLAT, MASK>,                               \
-   (const void*)&rg::k_wave<OP, T, OFFT, VEC, FLAT, MASK>,                                \
-   (const void*)&rg::k_block<OP, T, OFFT, VEC, FLAT, MASK>,                               \
-   (const void*)&rg::k_split_partial<OP, T, OFFT, VEC, FLAT, MASK>,                       \
-   (const void*)&rg::k_split_combine<OP, T, OFFT, VEC, FLAT, MASK>,                       \
+   (const void*)&rg::k_worker<OP, T, OFFT, VEC, FLAT, MASK>,                              \
    OP == rg::OP_SOFTMAX ? (const void*)&rg::k_split_normalize<OP, T, OFFT, VEC, FLAT, MASK> : nullptr, \
    rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, std::is_same<T, float>::value>(),              \
    rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, true>(),                                       \
@@ -91,7 +86,7 @@ const void* kernel_offsets_check(int offsets_dtype);
 #define RG_GEOMETRIES(OP, OFFT, MASK)                                                           \
   {{RG_SET(OP, float, OFFT, 1, false, MASK), RG_SET(OP, float, OFFT, 2, false, MASK),          \
     RG_SET(OP, float, OFFT, 4, false, MASK), RG_SET(OP, float, OFFT, 4, true, MASK),           \
-    {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                          \
+    {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                                      \
    {RG_SET(OP, __bf16, OFFT, 1, false, MASK), RG_SET(OP, __bf16, OFFT, 2, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 4, false, MASK), RG_SET(OP, __bf16, OFFT, 8, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 8, true, MASK)}}

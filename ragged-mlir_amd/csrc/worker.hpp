@@ -1,0 +1,364 @@
+// The classified schedule's worker for sum, max and the softmax that has no
+// register-resident worker (small or unvectorised feature widths).
+//
+// k_classify bins every segment into the wave, block and split queues
+// (reference ToGPU.cpp:901-998, wave64 thresholds). The reference then runs
+// one persistent kernel chain per class on forked streams
+// (ToGPU.cpp:999-1045, Driver.cpp:299-353). Here one persistent launch
+// drains all three by atomic ticket, longest work first:
+//   1. the parts of split segments; the part that arrives last at its
+//      segment's counter folds every part in part order (deterministic) and
+//      writes the result (sum, max) or the merged statistics (softmax, then
+//      normalised by k_split_normalize) -- the reference's split_combine
+//      (ToGPU.cpp:399-472) without a separate launch;
+//   2. block-class segments, one workgroup each;
+//   3. wave-class segments, 64 per wave. A segment of at most kLaneElems
+//      elements in the flat mapping (D below the vector width) is reduced by
+//      one lane on its own -- a batch of short segments costs one pass of
+//      64 lanes instead of 64 wave-wide reductions; longer ones are reduced
+//      by the whole wave, one after the other.
+#pragma once
+
+#include "kernels.hpp"
+
+namespace rg {
+
+// kLaneElems (flat elements one lane reduces on its own) is in device.hpp.
+
+// Agent-scope stores / loads of the split partials: parts run on any XCD,
+// and the last arriver must see every part's values.
+__device__ __forceinline__ void publish(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float fetch(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Feature tiles of a group of G threads (ROW mapping): lanes per row is
+// capped by G, and the remaining lanes of a row are further tiles.
+template <int VEC>
+__device__ __forceinline__ int tiles_of(int d, int g) {
+  const int lanes = (d + VEC - 1) / VEC;
+  const int lpr = lanes_per_row(d, VEC, g);
+  return (lanes + lpr - 1) / lpr;
+}
+
+// Vector j (elements j*VEC .. j*VEC + VEC - 1) of the flat input; a vector
+// that reaches past the last element (N*D not a multiple of VEC) is read
+// element by element, so no load leaves the array.
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void load_vector(const Params& p, int64_t j, float (&x)[VEC]) {
+  const int64_t total = p.n * p.d;
+  if ((j + 1) * VEC <= total) {
+    load_input<T, VEC, MASK>(p, j * VEC, x);
+  } else {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[c] = j * VEC + c < total ? load_input1<T, MASK>(p, j * VEC + c) : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One lane reduces elements [lo, hi) of a flat-mapped segment: aligned
+// VEC-element vectors, components outside [lo, hi) masked. Component c of
+// every vector is feature c % D (D divides VEC).
+
+template <int OP, class T, int VEC, bool MASK>
+__device__ __forceinline__ void lane_fold(const Params& p, int64_t lo, int64_t hi, State<OP> (&st)[VEC]) {
+  init_all<OP, VEC>(st);
+  if (lo >= hi) return;
+  const int64_t j0 = lo / VEC, j1 = (hi - 1) / VEC;
+  int64_t j = j0;
+  for (; j + 7 <= j1; j += 8) {
+    float x[8][VEC];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) load_vector<T, VEC, MASK>(p, j + u, x[u]);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        const int64_t e = (j + u) * VEC + c;
+        st[c].fold(e >= lo && e < hi ? x[u][c] : fold_identity<OP>());
+      }
+    }
+  }
+  for (; j <= j1; ++j) {
+    float x[VEC];
+    load_vector<T, VEC, MASK>(p, j, x);
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int64_t e = j * VEC + c;
+      st[c].fold(e >= lo && e < hi ? x[c] : fold_identity<OP>());
+    }
+  }
+}
+
+// Combines the components of each feature in place: component c holds
+// feature c % d (d a power of two dividing VEC). Afterwards every component
+// holds the combination of its feature's components, so no register array
+// is indexed by a run-time value.
+template <bool MAX, int VEC>
+__device__ __forceinline__ void fold_residues(float (&x)[VEC], int d) {
+#pragma unroll
+  for (int off = VEC / 2; off >= 1; off /= 2) {
+    if (off >= d) {
+#pragma unroll
+      for (int c = 0; c < off; ++c) x[c] = MAX ? fmax_nan(x[c], x[c + off]) : x[c] + x[c + off];
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < VEC; off *= 2) {
+    if (off >= d) {
+#pragma unroll
+      for (int c = 0; c < off; ++c) x[c + off] = x[c];
+    }
+  }
+}
+
+// Softmax of a flat-mapped segment by one lane: column max, column sum of
+// exp(x - ref) and the normalised values, three passes over its elements
+// (re-read from cache). A column of only -inf has no mass (ref 0).
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void lane_softmax(const Params& p, int64_t lo, int64_t hi) {
+  if (lo >= hi) return;
+  const int d = p.d;
+  const int64_t j0 = lo / VEC, j1 = (hi - 1) / VEC;
+  // Every pass visits the segment's vectors four at a time (four loads in
+  // flight per lane); a vector past j1 is not loaded.
+  auto pass = [&](auto&& body) {
+    for (int64_t j = j0; j <= j1; j += 4) {
+      float x[4][VEC];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (j + u <= j1) load_vector<T, VEC, MASK>(p, j + u, x[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (j + u <= j1) body(j + u, x[u]);
+      }
+    }
+  };
+  float m[VEC];   // per component; component c is feature c % d
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) m[c] = neg_inf();
+  pass([&](int64_t j, const float (&x)[VEC]) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int64_t e = j * VEC + c;
+      if (e >= lo && e < hi) m[c] = fmax_nan(m[c], x[c]);
+    }
+  });
+  fold_residues<true, VEC>(m, d);
+  float ref[VEC], s[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    ref[c] = m[c] == neg_inf() ? 0.f : m[c];
+    s[c] = 0.f;
+  }
+  pass([&](int64_t j, const float (&x)[VEC]) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int64_t e = j * VEC + c;
+      if (e >= lo && e < hi) s[c] += fast_exp(x[c] - ref[c]);
+    }
+  });
+  fold_residues<false, VEC>(s, d);
+  float inv[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) inv[c] = fast_exp(m[c] - m[c]) / s[c];   // 1 / s, or NaN for an all -inf column
+  T* out = static_cast<T*>(p.out);
+  pass([&](int64_t j, const float (&in)[VEC]) {
+    float x[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[c] = fast_exp(in[c] - ref[c]) * inv[c];
+    if (j * VEC >= lo && j * VEC + VEC <= hi) {
+      Elem<T>::template store<VEC>(out + j * VEC, x);   // a whole vector of this segment
+    } else {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        const int64_t e = j * VEC + c;
+        if (e >= lo && e < hi) Elem<T>::put(out + e, x[c]);
+      }
+    }
+  });
+}
+
+// A wave-class segment reduced by one lane (flat mapping).
+template <int OP, class T, int VEC, bool MASK>
+__device__ __forceinline__ void lane_segment(const Params& p, int64_t s, int64_t start, int64_t end) {
+  const int64_t lo = start * p.d, hi = end * p.d;
+  if constexpr (OP == OP_SOFTMAX) {
+    lane_softmax<T, VEC, MASK>(p, lo, hi);
+  } else {
+    State<OP> st[VEC];
+    lane_fold<OP, T, VEC, MASK>(p, lo, hi, st);
+    merge_components<OP, VEC>(st, p.d);
+    T* out = static_cast<T*>(p.out) + s * p.d;
+    for (int f = 0; f < p.d; ++f) Elem<T>::put(out + f, value_of<OP>(st[f]));
+  }
+  if (p.visits) atomicAdd(p.visits + s, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Split parts: the part's fold into partials[item] (agent scope), then the
+// last part of the segment to arrive folds all of them in part order.
+
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__device__ __forceinline__ void split_part(const Params& p, int64_t item, int tile, float* lds, int* flag_s) {
+  const int t = threadIdx.x;
+  int64_t k, s, part, start, end;
+  item_rows<OffT>(p, item, k, s, part, start, end);
+  State<OP> st[VEC];
+  init_all<OP, VEC>(st);
+  if constexpr (FLAT) {
+    fold_flat<OP, T, VEC, MASK>(p, kBlock, t, start * p.d, end * p.d, st);
+    merge_components<OP, VEC>(st, p.d);
+    block_reduce<OP, VEC>(st, 1, 0, lds);
+    if (t == 0) {
+      for (int f = 0; f < p.d; ++f) {
+        publish(p.partials + item * p.d + f, value_of<OP>(st[f]));
+        if constexpr (OP == OP_SOFTMAX) publish(p.partial_sums + item * p.d + f, st[f].s);
+      }
+    }
+  } else {
+    const RowGeo g = row_geo<VEC>(p.d, kBlock, t, tile);
+    fold_rows<OP, T, VEC, MASK>(p, g, start, end, st);
+    block_reduce<OP, VEC>(st, g.lpr, g.feat_lane, lds);
+    if (g.row_lane == 0 && g.active) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        if (g.feature + v < p.d) {
+          publish(p.partials + item * p.d + g.feature + v, value_of<OP>(st[v]));
+          if constexpr (OP == OP_SOFTMAX) publish(p.partial_sums + item * p.d + g.feature + v, st[v].s);
+        }
+      }
+    }
+  }
+  // Arrival: once this part's stores have completed (every thread waits
+  // for its own, then the barrier), count it at the segment.
+  int64_t seg_start, seg_end;
+  segment_rows<OffT>(p, s, seg_start, seg_end);
+  const int64_t all_parts = (seg_end - seg_start + p.part_rows - 1) / p.part_rows;
+  const int tiles = FLAT ? 1 : tiles_of<VEC>(p.d, kBlock);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == all_parts * tiles - 1;
+  __syncthreads();
+  const bool last = *flag_s != 0;
+  __syncthreads();
+  if (!last) return;
+  // Combine: threads = part lanes x features, LDS tree over part lanes, the
+  // parts folded in order within each lane and lanes in order.
+  const int64_t first = p.part_begin[k];
+  const int64_t stop = first + all_parts < p.items_cap ? first + all_parts : p.items_cap;
+  const int ft = combine_features(p.d);
+  const int pl_count = kBlock / ft;
+  const int fl = t % ft, pl = t / ft;
+  for (int64_t f0 = 0; f0 < p.d; f0 += ft) {
+    const int64_t f = f0 + fl;
+    State<OP> acc;
+    acc.init();
+    if (f < p.d) {
+      // Contiguous runs of parts per lane keep the fold in part order.
+      const int64_t count = stop - first;
+      const int64_t lo = first + count * pl / pl_count, hi = first + count * (pl + 1) / pl_count;
+      for (int64_t item2 = lo; item2 < hi; ++item2) {
+        if constexpr (OP == OP_SUM) {
+          acc.fold(fetch(p.partials + item2 * p.d + f));
+        } else {
+          State<OP> part_st;
+          part_st.m = fetch(p.partials + item2 * p.d + f);
+          if constexpr (OP == OP_SOFTMAX) part_st.s = fetch(p.partial_sums + item2 * p.d + f);
+          acc.merge(part_st);
+        }
+      }
+    }
+    st_write<OP>(lds + t, kBlock, acc);
+    __syncthreads();
+    if (pl == 0 && f < p.d) {
+      for (int q = 1; q < pl_count; ++q) acc.merge(st_read<OP>(lds + q * ft + fl, kBlock));
+      if constexpr (OP == OP_SOFTMAX) {
+        p.stats_max[k * p.d + f] = acc.m;
+        p.stats_sum[k * p.d + f] = acc.s;
+      } else {
+        Elem<T>::put(static_cast<T*>(p.out) + s * p.d + f, value_of<OP>(acc));
+      }
+    }
+    __syncthreads();
+  }
+  if constexpr (OP != OP_SOFTMAX) {
+    if (p.visits && t == 0) atomicAdd(p.visits + s, 1);
+  }
+}
+
+// ---------------------------------------------------------------------------
+
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__global__ __launch_bounds__(kBlock) void k_worker(Params p) {
+  __shared__ float lds[kBlock * VEC * 2];
+  __shared__ int64_t ticket_s;
+  __shared__ int flag_s;
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1), w = t / kWave;
+  const int tiles_block = FLAT ? 1 : tiles_of<VEC>(p.d, kBlock);
+  const int tiles_wave = FLAT ? 1 : tiles_of<VEC>(p.d, kWave);
+  // Ticket order: split parts (x feature tiles), block-class segments,
+  // batches of kWaveBatch wave-class segments.
+  // A wave-class batch: 64 segments per wave in the flat mapping (lane
+  // mode), one per wave otherwise (each is a wave-wide pass).
+  constexpr int kPerWave = FLAT ? kWave : 1;
+  constexpr int kBatch = kPerWave * kWavesPerBlock;
+  // Short-segment schedule: every segment, in order, is wave class; no
+  // counters, grid-stride batches.
+  const bool direct = p.short_segments != 0;
+  const int64_t n_items = direct ? 0 : (p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap);
+  const int64_t n_parts = n_items * tiles_block;
+  const int64_t n_block = direct ? 0 : p.counters[1];
+  const int64_t n_wave = direct ? p.b : p.counters[0];
+  const int64_t n_batches = (n_wave + kBatch - 1) / kBatch;
+  const int64_t total = n_parts + n_block + n_batches;
+  int64_t next = blockIdx.x;
+  for (;;) {
+    int64_t ticket = next;
+    if (!direct) {
+      __syncthreads();
+      if (t == 0) ticket_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+      __syncthreads();
+      ticket = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)ticket_s >> 32)) << 32) |
+                         __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)ticket_s));
+    }
+    next += gridDim.x;
+    if (ticket >= total) break;
+    if (ticket < n_parts) {
+      split_part<OP, T, OffT, VEC, FLAT, MASK>(p, ticket / tiles_block, (int)(ticket % tiles_block), lds, &flag_s);
+    } else if (ticket < n_parts + n_block) {
+      const int64_t s = p.queue[p.b + (ticket - n_parts)];
+      int64_t start, end;
+      segment_rows<OffT>(p, s, start, end);
+      // (process_segment counts a visit at tile 0 only.)
+      for (int tile = 0; tile < tiles_block; ++tile) process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, tile, lds);
+    } else {
+      // Wave-class batch: wave w takes kPerWave positions.
+      const int64_t pos = (ticket - n_parts - n_block) * kBatch + w * kPerWave + (kPerWave > 1 ? lane : 0);
+      const bool have = pos < n_wave && (kPerWave > 1 || lane == 0);
+      int64_t s = 0, start = 0, end = 0;
+      if (have) {
+        s = direct ? pos : p.queue[pos];
+        segment_rows<OffT>(p, s, start, end);
+      }
+      const bool alone = FLAT && have && (end - start) * p.d <= kLaneElems;
+      if constexpr (FLAT) {
+        if (alone) lane_segment<OP, T, VEC, MASK>(p, s, start, end);
+      }
+      uint64_t todo = __ballot(have && !alone);
+      while (todo) {
+        const int src = __ffsll((unsigned long long)todo) - 1;
+        todo &= todo - 1;
+        const int64_t ss = __shfl(s, src, kWave);
+        const int64_t a = __shfl(start, src, kWave), b = __shfl(end, src, kWave);
+        for (int tile = 0; tile < tiles_wave; ++tile) process_segment<OP, T, VEC, FLAT, MASK, false>(p, ss, a, b, tile, nullptr);
+      }
+    }
+  }
+}
+
+}  // namespace rg

@@ -22,9 +22,9 @@ ABI_VERSION = 1
 OPS = {"sum": 0, "max": 1, "softmax": 2}
 DTYPES = {"f32": 0, "bf16": 1}
 INDEX_DTYPES = {"i32": 0, "i64": 1}
-SCHEDULES = {"classified": 0, "naive": 1}
+SCHEDULES = {"classified": 0, "naive": 1, "short": 2}
 ROLES = ("init", "classify", "wave", "block", "split_partial", "split_combine", "split_normalize", "naive",
-         "fused", "deferred")
+         "fused", "deferred", "worker")
 BUFFERS = ("class_counts", "segment_ids", "item_segments", "part_begin", "partials", "partial_sums",
            "max_stats", "sum_stats", "visits", "deferred", "arrive", "segment_arrive", "items", "block_items",
            "pairs", "final_pairs")

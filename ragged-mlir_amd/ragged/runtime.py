@@ -78,7 +78,10 @@ class CompiledProgram:
             raise CacheMismatch("a block-per-segment companion must be the naive strategy of a classifying program")
         self.naive = naive
         self._choices: dict[tuple, tuple[str, dict[str, Any]]] = {}
-        self._plans: dict[tuple[int, int, int], native.Plan] = {}
+        self._plans: dict[tuple[int, int, int, str], native.Plan] = {}
+        # Workspace per (device, stream): calls on one stream run in order,
+        # so they can share it; it grows to the largest plan seen.
+        self._workspaces: dict[tuple[int, int], Any] = {}
         self._names = {kernel["role"]: kernel["name"] for kernel in self._metadata["kernels"]}
 
     @property
@@ -106,8 +109,27 @@ class CompiledProgram:
         return choice
 
     def close(self) -> None:
-        """Drop this program's plans; the shared native module stays loaded."""
+        """Drop this program's plans and workspaces; the shared native module
+        stays loaded."""
         self._plans.clear()
+        self._workspaces.clear()
+
+    def _workspace(self, torch, device, stream, nbytes: int, fresh: bool):
+        """Scratch of at least ``nbytes`` for a call on ``stream``. Calls on
+        one stream run in order, so they share one allocation (made on that
+        stream); ``fresh`` (debug buffers handed to the caller) allocates a
+        new one."""
+        if fresh:
+            with torch.cuda.stream(stream):
+                return torch.empty((nbytes,), dtype=torch.uint8, device=device)
+        key = (device.index if device.index is not None else 0, stream.cuda_stream)
+        workspace = self._workspaces.get(key)
+        if workspace is None or workspace.numel() < nbytes:
+            if len(self._workspaces) >= 16:
+                self._workspaces.clear()
+            with torch.cuda.stream(stream):
+                workspace = self._workspaces[key] = torch.empty((nbytes,), dtype=torch.uint8, device=device)
+        return workspace
 
     # ------------------------------------------------------------------
     def _validate_tensors(self, values, offsets, out, torch, *, checked: bool = False, mask=None) -> tuple[int, int]:
@@ -191,13 +213,13 @@ class CompiledProgram:
                 module = _modules[key] = native.NativeModule(device, spec)
             return module
 
-    def _plan(self, module: native.NativeModule, n: int, b: int) -> native.Plan:
-        key = (module.device, n, b)
+    def _plan(self, module: native.NativeModule, n: int, b: int, schedule: str) -> native.Plan:
+        key = (module.device, n, b, schedule)
         plan = self._plans.get(key)
         if plan is None:
             if len(self._plans) >= 256:
                 self._plans.clear()
-            plan = self._plans[key] = module.plan(n, b, self._schedule)
+            plan = self._plans[key] = module.plan(n, b, schedule)
         return plan
 
     # ------------------------------------------------------------------
@@ -234,7 +256,7 @@ class CompiledProgram:
         else:
             selection = {"forced": True} if self.naive is not None else {}
         return self._run(values, offsets, out, stream, mode, debug_buffers=debug_buffers, mask=mask,
-                         selected=self._schedule, selection=selection)
+                         selected=self._schedule, selection=selection, max_len=max_len)
 
     def _report(self, started, plan_names=(), grids=(), workspace=0, *, mode, selected, selection,
                 validation_bytes=0, validation_ms=None) -> ExecutionReport:
@@ -247,7 +269,17 @@ class CompiledProgram:
             optimizations=metadata["optimizations"], d_tile=metadata["d_tile"], d_vector=metadata["d_vector"],
             resources=None, streams=1, selected=selected, selection=selection)
 
-    def _run(self, values, offsets, out, stream, mode, *, debug_buffers, mask, selected, selection) -> ExecutionReport:
+    def _short_segments(self, max_len: int | None) -> bool:
+        """Whether the caller's max_len puts every segment in the wave class:
+        then one worker launch takes the segments in order (no classify, no
+        workspace). A max_len that is too small only costs time."""
+        thresholds = self._metadata["thresholds"]
+        return (self._schedule == "classified" and max_len is not None and not self._metadata["fused"]
+                and not self.spec.debug_visits and bool(thresholds) and 0 < thresholds[0]
+                and max_len <= thresholds[0])
+
+    def _run(self, values, offsets, out, stream, mode, *, debug_buffers, mask, selected, selection,
+             max_len: int | None = None) -> ExecutionReport:
         if mode not in ("validated", "checked"):
             raise ValidationError("mode must be validated or checked")
         if self.spec.mask != (mask is not None):
@@ -293,11 +325,14 @@ class CompiledProgram:
                 if b == 0:
                     return self._report(started, names, grids, 0, mode=mode, selected=selected, selection=selection,
                                         validation_bytes=validation_bytes, validation_ms=validation_ms)
-            plan = self._plan(module, n, b)
+            short = self._short_segments(max_len)
+            if short:
+                selection = {**selection, "short_segments": True}
+            plan = self._plan(module, n, b, "short" if short else self._schedule)
             workspace = None
             if plan.workspace_bytes:
-                with torch.cuda.stream(active):
-                    workspace = torch.empty((plan.workspace_bytes,), dtype=torch.uint8, device=values.device)
+                workspace = self._workspace(torch, values.device, active, int(plan.workspace_bytes),
+                                            fresh=debug_buffers is not None)
             inputs = [values, offsets, out] + ([mask] if mask is not None else [])
             for tensor in inputs:
                 tensor.record_stream(active)
@@ -325,9 +360,8 @@ class CompiledProgram:
 
     def _kernel_name(self, role: str) -> str:
         phase = "online" if self.spec.op == "softmax" else self.spec.op
-        manifest_role = {"wave": f"wave_{phase}", "block": f"block_{phase}",
-                         "split_partial": f"split_partial_{phase}", "split_combine": f"split_combine_{phase}",
-                         "naive": phase, "fused": "fused_online", "deferred": "deferred_online"}.get(role, role)
+        manifest_role = {"worker": f"worker_{phase}", "naive": phase, "fused": "fused_online",
+                         "deferred": "deferred_online"}.get(role, role)
         return self._names.get(manifest_role, f"ragged_0_{manifest_role}")
 
 

@@ -34,22 +34,21 @@ def _phase(op: str) -> str:
 
 
 def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> list[str]:
-    """Role names in launch order (reference naming, wave64 classes). With
-    ``fused`` the block and split classes of a softmax share one
-    register-resident worker plus its re-read pass."""
+    """Role names in launch order. The classified schedule runs init,
+    classify and one worker over the wave, block and split classes (plus the
+    split normalise pass of a softmax); with ``fused`` a softmax runs its
+    register-resident worker plus its re-read pass instead."""
     phase = _phase(spec.op)
     if classes == ["block"] and spec.strategy == "naive":
         return [phase]
     roles = ["init", "classify"]
     if fused:
         return roles + ["fused_online", "deferred_online"]
-    for segment_class in classes:
-        if segment_class == "split":
-            roles += [f"split_partial_{phase}", f"split_combine_{phase}"]
-            if spec.op == "softmax":
-                roles.append("split_normalize")
-        else:
-            roles.append(f"{segment_class}_{phase}")
+    # One persistent worker drains every class; the reference's per-class
+    # chains and split combine run inside it.
+    roles.append(f"worker_{phase}")
+    if "split" in classes and spec.op == "softmax":
+        roles.append("split_normalize")
     return roles
 
 

@@ -181,3 +181,32 @@ def test_unvectorized_unaligned_views(artifact_cache):
     values = np.random.default_rng(2).normal(size=(int(offsets[-1]), d)).astype(np.float32)
     actual, _ = run_program(program, values, offsets, dtype="f32", op="sum", select="classified")
     check(actual, values, offsets, op="sum", dtype="f32")
+
+
+@pytest.mark.parametrize("op", OPS)
+@pytest.mark.parametrize("d,dtype", [(1, "f32"), (2, "f32"), (4, "bf16"), (3, "f32"), (128, "f32"), (8, "bf16")])
+def test_short_segment_schedule(artifact_cache, op, d, dtype):
+    """With max_len at most the wave threshold one worker launch takes the
+    segments in order; a max_len below the true longest segment (a caller's
+    mistake) still gives exact results."""
+    program = program_for(artifact_cache, op, dtype, d, "i64")
+    t_wave = program.metadata["thresholds"][0]
+    if t_wave == 0:
+        pytest.skip("the register-resident softmax has no wave class")
+    rng = np.random.default_rng(40 + d)
+    lengths = rng.integers(0, t_wave + 1, size=3000).astype(np.int64)
+    lengths[::7] = 0
+    lengths[11] = t_wave
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified",
+                                 max_len=int(lengths.max()))
+    assert report.selection.get("short_segments") and len(report.kernel_names) == 1
+    assert report.workspace_bytes == 0
+    check(actual, values, offsets, op=op, dtype=dtype)
+    lengths[5] = 5 * t_wave + 17
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified", max_len=t_wave)
+    assert report.selection.get("short_segments")
+    check(actual, values, offsets, op=op, dtype=dtype)
