@@ -198,6 +198,70 @@ __device__ __forceinline__ void lane_segment(const Params& p, int64_t s, int64_t
   if (p.visits) atomicAdd(p.visits + s, 1);
 }
 
+// A wave-class segment in the row mapping reduced by a group of lanes that
+// together hold one row (lane `feature_lane` owns features feature_lane*VEC
+// .. +VEC): every lane walks all rows of the segment on its own, so no lane
+// waits for another; four rows' loads in flight per lane.
+template <int OP, class T, int VEC, bool MASK>
+__device__ __forceinline__ void group_segment(const Params& p, int64_t s, int64_t start, int64_t end,
+                                              int feature_lane) {
+  const int64_t d = p.d;
+  const int64_t f0 = (int64_t)feature_lane * VEC;
+  if (f0 < d) {
+    auto rows = [&](auto&& body) {
+      for (int64_t r = start; r < end; r += 4) {
+        float x[4][VEC];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (r + u < end) load_input<T, VEC, MASK>(p, (r + u) * d + f0, x[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (r + u < end) body(r + u, x[u]);
+        }
+      }
+    };
+    if constexpr (OP == OP_SOFTMAX) {
+      float m[VEC], sum[VEC], ref[VEC], inv[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        m[v] = neg_inf();
+        sum[v] = 0.f;
+      }
+      rows([&](int64_t, const float (&x)[VEC]) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) m[v] = fmax_nan(m[v], x[v]);
+      });
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) ref[v] = m[v] == neg_inf() ? 0.f : m[v];
+      rows([&](int64_t, const float (&x)[VEC]) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) sum[v] += fast_exp(x[v] - ref[v]);
+      });
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) inv[v] = fast_exp(m[v] - m[v]) / sum[v];   // NaN for an all -inf column
+      T* out = static_cast<T*>(p.out);
+      rows([&](int64_t r, const float (&x)[VEC]) {
+        float y[VEC];
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) y[v] = fast_exp(x[v] - ref[v]) * inv[v];
+        Elem<T>::template store<VEC>(out + r * d + f0, y);
+      });
+    } else {
+      State<OP> st[VEC];
+      init_all<OP, VEC>(st);
+      rows([&](int64_t, const float (&x)[VEC]) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) st[v].fold(x[v]);
+      });
+      float y[VEC];
+      result_of<OP, VEC>(st, y);
+      Elem<T>::template store<VEC>(static_cast<T*>(p.out) + s * d + f0, y);
+    }
+  }
+  if (p.visits && feature_lane == 0) atomicAdd(p.visits + s, 1);
+}
+
 // ---------------------------------------------------------------------------
 // Split parts: the part's fold into partials[item] (agent scope), then the
 // last part of the segment to arrive folds all of them in part order.
@@ -303,10 +367,12 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int tiles_wave = FLAT ? 1 : tiles_of<VEC>(p.d, kWave);
   // Ticket order: split parts (x feature tiles), block-class segments,
   // batches of kWaveBatch wave-class segments.
-  // A wave-class batch: 64 segments per wave in the flat mapping (lane
-  // mode), one per wave otherwise (each is a wave-wide pass).
-  constexpr int kPerWave = FLAT ? kWave : 1;
-  constexpr int kBatch = kPerWave * kWavesPerBlock;
+  // A wave-class batch: in the flat mapping 64 segments per wave, one per
+  // lane; in the row mapping one per group of the G lanes that hold a row
+  // (64 / G per wave), or one per wave when a row needs more than a wave.
+  const int group = FLAT ? 1 : (tiles_wave == 1 ? lanes_per_row(p.d, VEC, kWave) : kWave);
+  const int per_wave = kWave / group;
+  const int64_t batch = (int64_t)per_wave * kWavesPerBlock;
   // Short-segment schedule: every segment, in order, is wave class; no
   // counters, grid-stride batches.
   const bool direct = p.short_segments != 0;
@@ -314,7 +380,7 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int64_t n_parts = n_items * tiles_block;
   const int64_t n_block = direct ? 0 : p.counters[1];
   const int64_t n_wave = direct ? p.b : p.counters[0];
-  const int64_t n_batches = (n_wave + kBatch - 1) / kBatch;
+  const int64_t n_batches = (n_wave + batch - 1) / batch;
   const int64_t total = n_parts + n_block + n_batches;
   int64_t next = blockIdx.x;
   for (;;) {
@@ -337,19 +403,23 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
       // (process_segment counts a visit at tile 0 only.)
       for (int tile = 0; tile < tiles_block; ++tile) process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, tile, lds);
     } else {
-      // Wave-class batch: wave w takes kPerWave positions.
-      const int64_t pos = (ticket - n_parts - n_block) * kBatch + w * kPerWave + (kPerWave > 1 ? lane : 0);
-      const bool have = pos < n_wave && (kPerWave > 1 || lane == 0);
+      // Wave-class batch: wave w takes per_wave positions, one per group.
+      const int64_t pos = (ticket - n_parts - n_block) * batch + w * per_wave + lane / group;
+      const bool have = pos < n_wave;
       int64_t s = 0, start = 0, end = 0;
       if (have) {
         s = direct ? pos : p.queue[pos];
         segment_rows<OffT>(p, s, start, end);
       }
-      const bool alone = FLAT && have && (end - start) * p.d <= kLaneElems;
-      if constexpr (FLAT) {
-        if (alone) lane_segment<OP, T, VEC, MASK>(p, s, start, end);
+      // Reduced by its own lane / group when short (elements per lane at
+      // most kLaneElems), else by the whole wave.
+      const bool alone = have && (FLAT ? (end - start) * p.d : (end - start) * group) <= kLaneElems &&
+                         (FLAT || tiles_wave == 1);
+      if (alone) {
+        if constexpr (FLAT) lane_segment<OP, T, VEC, MASK>(p, s, start, end);
+        else group_segment<OP, T, VEC, MASK>(p, s, start, end, lane % group);
       }
-      uint64_t todo = __ballot(have && !alone);
+      uint64_t todo = __ballot(have && !alone && lane % group == 0);   // one bit per group
       while (todo) {
         const int src = __ffsll((unsigned long long)todo) - 1;
         todo &= todo - 1;

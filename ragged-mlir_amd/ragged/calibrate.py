@@ -1,0 +1,308 @@
+"""Cost-model calibration on MI355X: measure, fit, evaluate.
+
+Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
+272-305) and ``bench/suite.py`` (:42-60) for this build:
+
+* Two synthetic shape suites are fixed in code before any fit: ``train``
+  and ``heldout``, drawn from disjoint feature widths, sizes and seeds, so
+  no held-out shape is seen while fitting.
+* ``measure`` times both schedules (classified, block per segment) of every
+  case on the current GPU: complete ``program.run`` calls bracketed by
+  events on the calling stream, warm cache, median of repeated batches. It
+  appends one JSON line per case and skips cases already in the file, so an
+  interrupted run resumes.
+* ``fit`` solves, per operation family and schedule, a nonnegative least
+  squares problem on relative error (each row divided by its measured
+  time), choosing the subset of terms with the lowest leave-one-shape-out
+  error, and then the decision margin that maximises the share of training
+  cases within 3% of the faster schedule.
+* ``evaluate`` reports, for a suite's measurements, how many choices fall
+  within 3% of the faster measured schedule.
+
+    python -m ragged.calibrate measure --suite train --out train.jsonl
+    python -m ragged.calibrate fit train.jsonl --out cost_model.json
+    python -m ragged.calibrate evaluate heldout.jsonl [--model cost_model.json]
+"""
+from __future__ import annotations
+
+import argparse
+from dataclasses import asdict, dataclass
+import itertools
+import json
+import math
+from pathlib import Path
+import sys
+import time
+
+import numpy as np
+
+from .selection import FAMILIES, SCHEDULES, TERMS, VERSION, CostModel, family, features
+from .workloads import make_lengths, offsets_from_lengths
+
+WITHIN = 0.03     # a choice is good when its measured time is within 3% of the faster schedule
+
+
+@dataclass(frozen=True)
+class Case:
+    op: str
+    dtype: str
+    d: int
+    n: int                # rows
+    b: int                # segments
+    distribution: str
+    seed: int
+
+    @property
+    def key(self) -> str:
+        return f"{self.op}-{self.dtype}-d{self.d}-n{self.n}-b{self.b}-{self.distribution}-s{self.seed}"
+
+    @property
+    def element_bytes(self) -> int:
+        return 2 if self.dtype == "bf16" else 4
+
+
+def _grid(ds, elements, segments, seed0, count, seed_grid):
+    rng = np.random.default_rng(seed_grid)
+    grid = list(itertools.product(("sum", "max", "softmax"), ("f32", "bf16"), ds, elements, segments,
+                                  ("uniform", "long_tail", "bimodal", "burst", "exponential")))
+    picks = rng.choice(len(grid), size=min(count, len(grid)), replace=False)
+    cases = []
+    for i, index in enumerate(sorted(picks)):
+        op, dtype, d, total, b, dist = grid[index]
+        n = max(b, total // d)
+        cases.append(Case(op, dtype, int(d), int(n), int(b), dist, seed0 + i))
+    return cases
+
+
+def suite(name: str) -> list[Case]:
+    """The fixed shape suites. ``heldout`` shares no feature width, size or
+    segment count with ``train`` and reaches beyond the 256 MiB Infinity
+    Cache."""
+    if name == "train":
+        return _grid(ds=(1, 2, 8, 32, 128), elements=(1 << 18, 1 << 21, 1 << 24),
+                     segments=(256, 4096, 65536), seed0=1000, count=240, seed_grid=11)
+    if name == "heldout":
+        return _grid(ds=(4, 16, 64, 256), elements=(1 << 19, 1 << 22, 1 << 26),
+                     segments=(1024, 16384, 131072), seed0=5000, count=150, seed_grid=29)
+    raise ValueError("suite must be train or heldout")
+
+
+# ---------------------------------------------------------------------------
+# Measurement (GPU).
+
+def _time_calls(torch, run, repeats: int = 3, calls: int = 5) -> float:
+    """Median over ``repeats`` batches of the mean µs of ``calls`` complete calls."""
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    samples = []
+    for _ in range(repeats):
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(calls):
+            run()
+        end.record()
+        torch.cuda.synchronize()
+        samples.append(start.elapsed_time(end) * 1e3 / calls)
+    return float(np.median(samples))
+
+
+def measure(cases: list[Case], out: Path, *, log=print) -> int:
+    """Time both schedules of every case not yet in ``out``; returns how many
+    were measured now."""
+    import tempfile
+
+    import torch
+
+    from . import ArtifactCache, Compiler, ProgramSpec
+
+    done = set()
+    if out.exists():
+        for line in out.read_text().splitlines():
+            if line.strip():
+                done.add(json.loads(line)["key"])
+    device = torch.device("cuda", 0)
+    generator = torch.Generator(device=device)
+    programs: dict[tuple, object] = {}
+    cache = ArtifactCache(tempfile.mkdtemp(prefix="ragged-calibrate-"))
+    measured = 0
+    with out.open("a") as sink:
+        for case in cases:
+            if case.key in done:
+                continue
+            lengths = make_lengths(case.distribution, case.b, seed=case.seed, total_elements=case.n)
+            offsets = offsets_from_lengths(lengths, "i64")
+            generator.manual_seed(case.seed)
+            tdtype = torch.bfloat16 if case.dtype == "bf16" else torch.float32
+            x = torch.randn((case.n, case.d), generator=generator, device=device).to(tdtype)
+            off = torch.from_numpy(offsets).to(device)
+            out_rows = case.n if case.op == "softmax" else case.b
+            y = torch.empty((out_rows, case.d), dtype=tdtype, device=device)
+            key = (case.op, case.dtype, case.d)
+            if key not in programs:
+                programs[key] = Compiler().compile(ProgramSpec(case.op, case.dtype, case.d, "i64"), cache)
+            program = programs[key]
+            max_len = int(lengths.max())
+            times = {}
+            for schedule in SCHEDULES:
+                run = lambda: program.run(x, off, y, select=schedule, max_len=max_len)   # noqa: E731
+                run()
+                times[schedule] = round(_time_calls(torch, run), 2)
+            record = {**asdict(case), "key": case.key, "max_len": max_len, "us": times}
+            sink.write(json.dumps(record) + "\n")
+            sink.flush()
+            measured += 1
+            log(f"[calibrate] {case.key}: classified {times['classified']} us, naive {times['naive']} us")
+            del x, y, off
+    return measured
+
+
+# ---------------------------------------------------------------------------
+# Fit and evaluation (CPU).
+
+def load(path: Path) -> list[dict]:
+    return [json.loads(line) for line in Path(path).read_text().splitlines() if line.strip()]
+
+
+def _row(record: dict) -> np.ndarray:
+    element = 2 if record["dtype"] == "bf16" else 4
+    return np.array(features(record["n"], record["b"], record["d"], record["max_len"], element, record["op"]))
+
+
+def _nnls(a: np.ndarray, y: np.ndarray) -> np.ndarray:
+    from scipy.optimize import nnls
+    scale = np.maximum(np.abs(a).max(axis=0), 1e-12)
+    coef, _ = nnls(a / scale, y)
+    return coef / scale
+
+
+def _fit_relative(rows: np.ndarray, times: np.ndarray, mask: tuple[bool, ...]) -> np.ndarray:
+    """NNLS on relative error over the terms in ``mask`` (others zero)."""
+    cols = [i for i in range(TERMS) if mask[i]]
+    a = rows[:, cols] / times[:, None]
+    coef = np.zeros(TERMS)
+    coef[cols] = _nnls(a, np.ones(len(times)))
+    return coef
+
+
+def _shape_key(record: dict) -> tuple:
+    return (record["op"], record["dtype"], record["d"], record["n"], record["b"])
+
+
+def fit_family(records: list[dict], schedule: str) -> tuple[np.ndarray, float]:
+    """Coefficients for one family and schedule: the term subset (constant
+    always in) with the lowest leave-one-shape-out mean relative error."""
+    rows = np.array([_row(r) for r in records])
+    times = np.array([r["us"][schedule] for r in records], dtype=np.float64)
+    shapes = [_shape_key(r) for r in records]
+    groups = sorted(set(shapes))
+    best, best_error = None, math.inf
+    for bits in range(1 << (TERMS - 1)):
+        mask = (True,) + tuple(bool(bits >> i & 1) for i in range(TERMS - 1))
+        errors = []
+        for group in groups:
+            train = np.array([s != group for s in shapes])
+            if train.sum() < sum(mask):
+                continue
+            coef = _fit_relative(rows[train], times[train], mask)
+            test = ~train
+            errors.extend(np.abs(rows[test] @ coef - times[test]) / times[test])
+        error = float(np.mean(errors)) if errors else math.inf
+        if error < best_error:
+            best, best_error = mask, error
+    return _fit_relative(rows, times, best), best_error
+
+
+def choices(model: CostModel, records: list[dict]) -> list[tuple[dict, str]]:
+    out = []
+    for record in records:
+        element = 2 if record["dtype"] == "bf16" else 4
+        chosen, _ = model.choose(record["op"], record["n"], record["b"], record["d"], record["max_len"], element)
+        out.append((record, chosen))
+    return out
+
+
+def evaluate(model: CostModel, records: list[dict]) -> dict:
+    """Share of choices within 3% of the faster measured schedule, overall
+    and per family, with the slowdown of every miss."""
+    good, misses, per_family = 0, [], {f: [0, 0] for f in FAMILIES}
+    for record, chosen in choices(model, records):
+        times = record["us"]
+        best = min(times.values())
+        ok = times[chosen] <= best * (1 + WITHIN)
+        good += ok
+        per_family[family(record["op"])][0] += ok
+        per_family[family(record["op"])][1] += 1
+        if not ok:
+            misses.append({"key": record["key"], "chosen": chosen, "us": times,
+                           "slowdown": round(times[chosen] / best, 3)})
+    return {"cases": len(records), "within_3pct": good, "share": round(good / max(len(records), 1), 4),
+            "per_family": {f: {"within_3pct": v[0], "cases": v[1]} for f, v in per_family.items()},
+            "misses": misses}
+
+
+def fit(records: list[dict]) -> dict:
+    """The cost model file for ``records`` (train measurements)."""
+    coefficients, errors = {}, {}
+    for name in FAMILIES:
+        subset = [r for r in records if family(r["op"]) == name]
+        if len(subset) < TERMS:
+            raise ValueError(f"too few {name} measurements to fit ({len(subset)})")
+        coefficients[name], errors[name] = {}, {}
+        for schedule in SCHEDULES:
+            coef, error = fit_family(subset, schedule)
+            coefficients[name][schedule] = [round(float(c), 6) for c in coef]
+            errors[name][schedule] = round(error, 4)
+    data = {"version": VERSION, "coefficients": coefficients, "margin": 0.0, "l2_mib": 32.0, "mall_mib": 256.0,
+            "calibration": {}}
+    # Margin: classify only when predicted faster by this fraction; pick the
+    # one that maximises within-3% choices on the training set.
+    best_margin, best_share = 0.0, -1.0
+    for margin in np.arange(0.0, 0.5, 0.01):
+        data["margin"] = float(round(margin, 2))
+        share = evaluate(CostModel.from_dict(data), records)["share"]
+        if share > best_share + 1e-12:
+            best_margin, best_share = data["margin"], share
+    data["margin"] = best_margin
+    data["calibration"] = {
+        "status": "fitted on MI355X measurements (python -m ragged.calibrate fit)",
+        "terms": "t_us = c0 + c1*M + c2*S + c3*B/1000 + c4*M*log2(skew) + c5*X_l2 + c6*X_mall",
+        "method": "per family and schedule: NNLS on relative error, term subset by leave-one-shape-out error; "
+                  "margin maximising training choices within 3% of the faster schedule",
+        "train_cases": len(records), "leave_one_shape_out_error": errors, "train_within_3pct": best_share}
+    return data
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = parser.add_subparsers(dest="command", required=True)
+    m = sub.add_parser("measure")
+    m.add_argument("--suite", choices=("train", "heldout"), required=True)
+    m.add_argument("--out", type=Path, required=True)
+    m.add_argument("--limit", type=int, help="measure at most this many cases of the suite")
+    f = sub.add_parser("fit")
+    f.add_argument("results", type=Path)
+    f.add_argument("--out", type=Path, required=True)
+    e = sub.add_parser("evaluate")
+    e.add_argument("results", type=Path)
+    e.add_argument("--model", type=Path)
+    args = parser.parse_args(argv)
+    if args.command == "measure":
+        cases = suite(args.suite)[: args.limit]
+        started = time.perf_counter()
+        count = measure(cases, args.out, log=lambda s: print(s, flush=True))
+        print(f"[calibrate] measured {count} cases in {time.perf_counter() - started:.1f}s", flush=True)
+        return 0
+    if args.command == "fit":
+        data = fit(load(args.results))
+        args.out.write_text(json.dumps(data, indent=2) + "\n")
+        print(json.dumps(data["calibration"], indent=2))
+        return 0
+    model = CostModel.load(args.model) if args.model else CostModel.load()
+    report = evaluate(model, load(args.results))
+    print(json.dumps({k: v for k, v in report.items() if k != "misses"}, indent=2))
+    for miss in report["misses"]:
+        print(json.dumps(miss))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

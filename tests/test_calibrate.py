@@ -1,0 +1,68 @@
+"""CPU tests of the cost-model calibration (reference test_calibrate.py:16-41:
+known coefficients are recovered from synthetic timings) and of the fixed
+suites it measures."""
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+
+from ragged import calibrate
+from ragged.selection import CostModel, features
+
+TRUTH = {"reduce": {"classified": [20.0, 0.0, 0.0, 0.5, 0.0, 0.0, 0.0],
+                    "naive": [8.0, 0.0, 30.0, 2.0, 0.0, 0.0, 0.0]},
+         "softmax": {"classified": [25.0, 0.0, 0.0, 0.8, 0.0, 0.0, 0.0],
+                     "naive": [8.0, 0.0, 60.0, 3.0, 0.0, 0.0, 0.0]}}
+
+
+def synthetic_records(cases, truth):
+    records = []
+    for case in cases:
+        # Lengths are not generated here: max_len from the distribution's cap.
+        max_len = case.n if case.distribution == "burst" else max(1, case.n // case.b * 8)
+        row = np.array(features(case.n, case.b, case.d, max_len, case.element_bytes, case.op))
+        fam = "softmax" if case.op == "softmax" else "reduce"
+        us = {s: float(row @ np.array(truth[fam][s])) for s in ("classified", "naive")}
+        records.append({**case.__dict__, "key": case.key, "max_len": max_len, "us": us})
+    return records
+
+
+def test_suites_are_fixed_and_disjoint():
+    train, heldout = calibrate.suite("train"), calibrate.suite("heldout")
+    assert train == calibrate.suite("train") and len(train) == 240 and len(heldout) == 150
+    assert {c.d for c in train}.isdisjoint({c.d for c in heldout})
+    assert {c.key for c in train}.isdisjoint({c.key for c in heldout})
+    # Some held-out working sets (rows read plus rows written) exceed the
+    # 256 MiB Infinity Cache.
+    assert any(c.n * c.d * c.element_bytes * (2 if c.op == "softmax" else 1) > 256 << 20 for c in heldout)
+
+
+def test_fit_recovers_known_coefficients():
+    records = synthetic_records(calibrate.suite("train")[::3], TRUTH)
+    data = calibrate.fit(records)
+    model = CostModel.from_dict(data)
+    for record in records[:20]:
+        for schedule in ("classified", "naive"):
+            predicted = model.predict(schedule, record["op"], record["n"], record["b"], record["d"],
+                                      record["max_len"], 2 if record["dtype"] == "bf16" else 4)
+            assert predicted == pytest.approx(record["us"][schedule], rel=1e-3)
+    assert calibrate.evaluate(model, records)["share"] == 1.0
+
+
+def test_evaluate_counts_within_three_percent():
+    records = synthetic_records(calibrate.suite("heldout")[:10], TRUTH)
+    model = CostModel.from_dict({"version": 3, "coefficients": TRUTH, "margin": 0.0, "l2_mib": 32.0,
+                                 "mall_mib": 256.0})
+    report = calibrate.evaluate(model, records)
+    assert report["within_3pct"] == 10 and not report["misses"]
+    # A model that always picks the slower schedule misses every case where
+    # the schedules differ by more than 3%.
+    swapped = json.loads(json.dumps(TRUTH))
+    for fam in swapped:
+        swapped[fam]["classified"], swapped[fam]["naive"] = TRUTH[fam]["naive"], TRUTH[fam]["classified"]
+    bad = CostModel.from_dict({"version": 3, "coefficients": swapped, "margin": 0.0, "l2_mib": 32.0,
+                               "mall_mib": 256.0})
+    expected = sum(1 for r in records if max(r["us"].values()) > min(r["us"].values()) * 1.03)
+    assert len(calibrate.evaluate(bad, records)["misses"]) == expected
