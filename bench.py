@@ -119,14 +119,17 @@ def cpu_baseline(op, dtype, values_f32, offsets, *, target_seconds=15.0):
 def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_wave: int, t_block: int,
                offset_bytes: int = 8) -> int:
     """Algorithmic bytes of the rows one kernel role owns. The
-    register-resident softmax ("fused") reads every row once and writes every
-    row once: the whole call's value bytes. Its re-read pass ("deferred")
-    moves no algorithmic bytes; "classify" reads the offsets."""
+    register-resident softmax ("fused") reads and writes every row of the
+    segments longer than t_wave once; after it "deferred" does the same for
+    the wave class (its re-read of deferred chunks is not algorithmic);
+    "classify" reads the offsets."""
     if role == "fused":
-        return 2 * int(lengths.sum()) * d * element
+        return 2 * int(lengths[lengths > t_wave].sum()) * d * element
+    if role == "deferred":
+        return 2 * int(lengths[lengths <= t_wave].sum()) * d * element
     if role == "classify":
         return (len(lengths) + 1) * offset_bytes
-    if role in ("init", "deferred"):
+    if role == "init":
         return 0
     if role == "worker":
         # The classified worker reads every row once; it writes every

@@ -44,8 +44,8 @@ enum rg_index { RG_I32 = 0, RG_I64 = 1 };
 /* RG_SHORT_SEGMENTS: every segment is expected to be at most t_wave rows
  * (the caller's max_len says so): one worker launch takes the segments in
  * order, with no classification and no workspace. Any input is still
- * computed exactly; a longer segment only runs slower. Not available for the
- * register-resident softmax (its t_wave is 0). */
+ * computed exactly; a longer segment only runs slower. Not available when
+ * t_wave is 0. */
 enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1, RG_SHORT_SEGMENTS = 2 };
 
 /* Kernel roles, in launch order of the classified schedule. */
@@ -119,7 +119,9 @@ typedef struct rg_plan {
 
 /* Workspace buffer indices (rg_plan.buffer_offset / buffer_bytes). */
 enum rg_buffer {
-  RG_BUF_COUNTERS = 0,      /* i64[8] class counts, split items, work ticket, deferred count */
+  RG_BUF_COUNTERS = 0,      /* i64[8] wave/block/split counts, split items, work ticket, deferred
+                               count, tree items; slot 7: the wave count of a register-resident
+                               softmax (whose slot 0 stays 0) */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class */
   RG_BUF_ITEM_POS = 2,      /* i64[items_cap] split position of each item */
   RG_BUF_PART_BEGIN = 3,    /* i64[B_split] first item of each split segment */

@@ -171,11 +171,16 @@ int rg_spec_defaults(rg_spec* spec) {
   const int64_t row = (int64_t)spec->feature_dim * element_bytes(spec->dtype);
   const bool default_wave = spec->t_wave < 0;
   const Geometry geo = choose_geometry(spec->dtype, spec->feature_dim, spec->vectorize != 0);
-  // Wave class: in the flat mapping (D below the vector width) the segments
-  // one lane reduces on its own, else what one wave reads in one pass.
-  if (default_wave)
+  // Wave class: the segments one lane (flat mapping, D below the vector
+  // width) or one group of a row's lanes (row mapping, rows narrower than a
+  // wave) reduces on its own; with rows as wide as a wave, what one wave
+  // reads in one pass.
+  if (default_wave) {
+    const int64_t lanes = (spec->feature_dim + geo.vec - 1) / geo.vec;
     spec->t_wave = geo.flat ? std::max<int64_t>(1, rg::kLaneElems / spec->feature_dim)
-                            : std::max<int64_t>(1, kWaveBytes / row);
+                 : lanes < rg::kWave ? rg::kGroupRows
+                                     : std::max<int64_t>(1, kWaveBytes / row);
+  }
   // Softmax with a register-resident worker: a block-class segment and a
   // split chunk are exactly what one workgroup holds in registers.
   const int64_t capacity = spec->op == RG_OP_SOFTMAX
@@ -183,11 +188,10 @@ int rg_spec_defaults(rg_spec* spec) {
                        spec->has_mask != 0 || spec->scale != 1.0f)
       : 0;
   if (capacity > 0) {
-    // The register-resident path has no wave class: t_wave 0 (empty
-    // segments only, which it also takes).
-    if (default_wave && spec->t_block < 0) spec->t_wave = 0;
     if (spec->t_block < 0) spec->t_block = capacity;
     if (spec->part_rows < 0) spec->part_rows = capacity;
+    // The wave class stays with the streaming worker, below the block class.
+    if (default_wave) spec->t_wave = std::max<int64_t>(0, std::min<int64_t>(spec->t_wave, spec->t_block - 1));
   }
   if (spec->t_block < 0) spec->t_block = std::max<int64_t>(spec->t_wave + 1, kBlockBytes / row);
   if (spec->part_rows < 0) spec->part_rows = std::max<int64_t>(1, kPartBytes / row);
@@ -377,7 +381,7 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   if (b == 0 && n != 0) return fail(RG_E_INVALID, "B=0 requires N=0");
   if (schedule != RG_CLASSIFIED && schedule != RG_BLOCK_PER_SEGMENT && schedule != RG_SHORT_SEGMENTS)
     return fail(RG_E_INVALID, "unknown schedule");
-  if (schedule == RG_SHORT_SEGMENTS && (module->fused || module->spec.t_wave < 1))
+  if (schedule == RG_SHORT_SEGMENTS && module->spec.t_wave < 1)
     return fail(RG_E_INVALID, "this specialisation has no short-segment schedule");
   if (schedule == RG_BLOCK_PER_SEGMENT && module->spec.debug_visits)
     return fail(RG_E_INVALID, "debug visits require the classified schedule");
@@ -413,10 +417,13 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     add_launch(RG_ROLE_NAIVE, b, tiles_block);
     return RG_OK;
   }
+  // Workgroups for grid-stride batches of at most B wave-class segments:
+  // the fewest segments a workgroup takes per batch is one per wave.
+  const int64_t wave_batch_min = geo.flat ? rg::kBlock : rg::kWavesPerBlock;
+  const int64_t stride_grid = (b + wave_batch_min - 1) / wave_batch_min;
   if (schedule == RG_SHORT_SEGMENTS) {
     // Batches of segments in order, grid-stride: no counters, no workspace.
-    const int64_t batch = geo.flat ? rg::kBlock : rg::kWavesPerBlock;
-    add_launch(RG_ROLE_WORKER, std::min(module->resident[RG_ROLE_WORKER], (b + batch - 1) / batch), 1);
+    add_launch(RG_ROLE_WORKER, std::min(module->resident[RG_ROLE_WORKER], stride_grid), 1);
     return RG_OK;
   }
 
@@ -474,8 +481,10 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, init_work / (rg::kBlock * 8))), 1);
   add_launch(RG_ROLE_CLASSIFY, (b + rg::kBlock - 1) / rg::kBlock, 1);
   if (module->fused) {
+    // The block and split classes held in registers; then the deferred
+    // chunks and the wave class, in the streaming worker's batches.
     add_launch(RG_ROLE_FUSED, std::min(module->resident[RG_ROLE_FUSED], b + items_cap), 1);
-    if (b_split) add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], items_cap), 1);
+    add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], std::max(items_cap, stride_grid)), 1);
     return RG_OK;
   }
   // One persistent worker drains the wave, block and split queues (as many

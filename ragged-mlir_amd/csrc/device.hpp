@@ -36,7 +36,8 @@ constexpr int kBlock = 256;            // threads of every workgroup-level worke
 constexpr int kWavesPerBlock = kBlock / kWave;
 constexpr int kUnroll = 4;             // rows (or flat vectors) loaded per lane before folding
 constexpr int kCombineFeatures = 64;   // consecutive features per split-combine pass
-constexpr int kLaneElems = 256;        // classified worker: flat elements one lane reduces alone
+constexpr int kLaneElems = 64;         // classified worker: flat elements one lane reduces alone
+constexpr int kGroupRows = 32;         // classified worker: rows one lane group walks alone
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
@@ -74,7 +75,8 @@ struct Params {
   int64_t items_cap;       // capacity of the split item tables
   int64_t b_split;         // capacity of the split queue / statistics rows
   int64_t* counters;       // [8]: wave, block, split segment counts; split items;
-                           //      work ticket; deferred chunks
+                           //      work ticket; deferred chunks; tree items; wave
+                           //      count of a register-resident softmax
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item
   int64_t* part_begin;     // [B] first item of each split-queue position

@@ -30,7 +30,7 @@
 
 #include <type_traits>
 
-#include "kernels.hpp"
+#include "worker.hpp"
 
 namespace rg {
 
@@ -365,7 +365,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
   // Ticket order: chunks of segments merged by tree (top of the item
   // array), chunks of segments merged directly (bottom), block-class
-  // segments, wave-class segments (far end of block_items).
+  // segments, wave-class segments (far end of block_items). k_classify
+  // counts a register-resident program's wave class in counters[7] instead
+  // of counters[0] -- k_softmax_deferred takes it after this kernel -- so
+  // the last term is 0. It stays: without it the compiler allocates this
+  // kernel's scalar registers differently and it runs slower.
   const int64_t n_tree = p.counters[6] < p.items_cap ? p.counters[6] : p.items_cap;
   const int64_t n_direct = p.counters[3] < p.items_cap - n_tree ? p.counters[3] : p.items_cap - n_tree;
   const int64_t n_split = n_tree + n_direct;
@@ -590,6 +594,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
 // Chunks that did not normalise in k_softmax_fused (spin limit, or a segment
 // longer than the device holds at once): re-read and normalise with the
 // segment's merged statistics, complete once k_softmax_fused has finished.
+// Then the wave class, which k_softmax_fused does not take (k_classify
+// counts it in counters[7]), in the streaming worker's batches: a ticket per
+// short segment would serialise k_softmax_fused on its ticket counter.
 template <class T, class OffT, int VEC, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
   const int64_t count = p.counters[5] < p.items_cap ? p.counters[5] : p.items_cap;
@@ -616,6 +623,10 @@ __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
     if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     __syncthreads();
   }
+  const int64_t n_wave = p.counters[7];
+  const int64_t batch = wave_batch_size<false, VEC>(p.d);
+  for (int64_t i = blockIdx.x; i * batch < n_wave; i += gridDim.x)
+    wave_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_wave, false);
 }
 
 }  // namespace rg

@@ -13,6 +13,8 @@
 //    k_split_normalize writes the probabilities (ToGPU.cpp:279-281).
 #pragma once
 
+#include <type_traits>
+
 #include "device.hpp"
 
 namespace rg {
@@ -20,11 +22,16 @@ namespace rg {
 // ---------------------------------------------------------------------------
 // Input transformation: f32(value) * scale + mask (docs/mask-abi.md:28-43).
 
+// bf16 values are scaled unconditionally (p.scale is 1 without one, and
+// x * 1 is x exactly): a branch here would end the basic block after every
+// load, and the conversion of the loaded words could then not move below
+// the next load -- each load of an unrolled loop would wait for the one
+// before. f32 values need no conversion, and skip the multiply.
 template <class T, int VEC, bool MASK>
 __device__ __forceinline__ void load_input(const Params& p, int64_t element, float (&x)[VEC]) {
 #pragma clang fp contract(off)
   Elem<T>::template load<VEC>(static_cast<const T*>(p.values) + element, x);
-  if (p.has_scale) {
+  if (!std::is_same<T, float>::value || p.has_scale) {
 #pragma unroll
     for (int v = 0; v < VEC; ++v) x[v] = x[v] * p.scale;
   }
@@ -39,8 +46,7 @@ __device__ __forceinline__ void load_input(const Params& p, int64_t element, flo
 template <class T, bool MASK>
 __device__ __forceinline__ float load_input1(const Params& p, int64_t element) {
 #pragma clang fp contract(off)
-  float x = Elem<T>::get(static_cast<const T*>(p.values) + element);
-  if (p.has_scale) x = x * p.scale;
+  float x = Elem<T>::get(static_cast<const T*>(p.values) + element) * p.scale;
   if constexpr (MASK) x = x + p.mask[element];
   return x;
 }
@@ -448,7 +454,11 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
     const int c = threadIdx.x;
     long long total = 0;
     for (int w = 0; w < kWavesPerBlock; ++w) total += run_s[c][w];
-    long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + c), (unsigned long long)total) : 0;
+    // A register-resident softmax (block_items set) counts its wave class
+    // in counters[7]: k_softmax_deferred takes it, and k_softmax_fused,
+    // which reads counters[0], sees none.
+    const int slot = c == 0 && p.block_items ? 7 : c;
+    long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + slot), (unsigned long long)total) : 0;
     for (int w = 0; w < kWavesPerBlock; ++w) {
       const long long count = run_s[c][w];
       run_s[c][w] = base;
@@ -463,10 +473,8 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
     if (ballot == 0) continue;
     const int64_t pos = run_s[c][wave] + __popcll(ballot & below);
     if (mine) p.queue[c * p.b + pos] = s;
-    // Register-resident softmax: whole segments of the wave and block
-    // classes are items too (wave class from the far end of the array).
-    if (mine && c < 2 && p.block_items)
-      p.block_items[c == 1 ? pos : p.b - 1 - pos] = Item{start, s, (int32_t)length, -1, 0, 1};
+    // Register-resident softmax: whole block-class segments are items too.
+    if (mine && c == 1 && p.block_items) p.block_items[pos] = Item{start, s, (int32_t)length, -1, 0, 1};
     if (c != 2) continue;
     // Split segments reserve ceil(L / part_rows) consecutive items. Valid
     // offsets never put more than b_split segments in the split queue;

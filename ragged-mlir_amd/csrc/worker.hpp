@@ -43,17 +43,39 @@ __device__ __forceinline__ int tiles_of(int d, int g) {
   return (lanes + lpr - 1) / lpr;
 }
 
-// Vector j (elements j*VEC .. j*VEC + VEC - 1) of the flat input; a vector
-// that reaches past the last element (N*D not a multiple of VEC) is read
-// element by element, so no load leaves the array.
-template <class T, int VEC, bool MASK>
-__device__ __forceinline__ void load_vector(const Params& p, int64_t j, float (&x)[VEC]) {
-  const int64_t total = p.n * p.d;
-  if ((j + 1) * VEC <= total) {
-    load_input<T, VEC, MASK>(p, j * VEC, x);
-  } else {
+// Vectors j0 .. j1 (elements j*VEC .. j*VEC + VEC - 1) of the flat input,
+// U at a time: body(j, x) for each. Whole vectors are loaded U at a time
+// with no branch between the loads, so they are all in flight together; in
+// the last round, short of U, a load past jv re-reads vector jv (in cache)
+// and is not passed on. The one vector that reaches past the array's last
+// element (N*D not a multiple of VEC) is read element by element, so no
+// load leaves the array.
+template <int U, class T, int VEC, bool MASK, class Body>
+__device__ __forceinline__ void flat_vectors(const Params& p, int64_t j0, int64_t j1, Body&& body) {
+  const int64_t total = p.n * p.d, full = total / VEC;
+  const int64_t jv = j1 < full ? j1 : full - 1;     // last whole vector
+  int64_t j = j0;
+  for (; j + (U - 1) <= jv; j += U) {
+    float x[U][VEC];
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) x[c] = j * VEC + c < total ? load_input1<T, MASK>(p, j * VEC + c) : 0.f;
+    for (int u = 0; u < U; ++u) load_input<T, VEC, MASK>(p, (j + u) * VEC, x[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) body(j + u, x[u]);
+  }
+  if (j <= jv) {
+    float x[U][VEC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_input<T, VEC, MASK>(p, (j + u <= jv ? j + u : jv) * VEC, x[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j + u <= jv) body(j + u, x[u]);
+    }
+  }
+  if (j1 > jv) {
+    float x[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) x[c] = j1 * VEC + c < total ? load_input1<T, MASK>(p, j1 * VEC + c) : 0.f;
+    body(j1, x);
   }
 }
 
@@ -66,30 +88,13 @@ template <int OP, class T, int VEC, bool MASK>
 __device__ __forceinline__ void lane_fold(const Params& p, int64_t lo, int64_t hi, State<OP> (&st)[VEC]) {
   init_all<OP, VEC>(st);
   if (lo >= hi) return;
-  const int64_t j0 = lo / VEC, j1 = (hi - 1) / VEC;
-  int64_t j = j0;
-  for (; j + 7 <= j1; j += 8) {
-    float x[8][VEC];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) load_vector<T, VEC, MASK>(p, j + u, x[u]);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        const int64_t e = (j + u) * VEC + c;
-        st[c].fold(e >= lo && e < hi ? x[u][c] : fold_identity<OP>());
-      }
-    }
-  }
-  for (; j <= j1; ++j) {
-    float x[VEC];
-    load_vector<T, VEC, MASK>(p, j, x);
+  flat_vectors<8, T, VEC, MASK>(p, lo / VEC, (hi - 1) / VEC, [&](int64_t j, const float (&x)[VEC]) {
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int64_t e = j * VEC + c;
       st[c].fold(e >= lo && e < hi ? x[c] : fold_identity<OP>());
     }
-  }
+  });
 }
 
 // Combines the components of each feature in place: component c holds
@@ -123,20 +128,8 @@ __device__ __forceinline__ void lane_softmax(const Params& p, int64_t lo, int64_
   const int d = p.d;
   const int64_t j0 = lo / VEC, j1 = (hi - 1) / VEC;
   // Every pass visits the segment's vectors four at a time (four loads in
-  // flight per lane); a vector past j1 is not loaded.
-  auto pass = [&](auto&& body) {
-    for (int64_t j = j0; j <= j1; j += 4) {
-      float x[4][VEC];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (j + u <= j1) load_vector<T, VEC, MASK>(p, j + u, x[u]);
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (j + u <= j1) body(j + u, x[u]);
-      }
-    }
-  };
+  // flight per lane).
+  auto pass = [&](auto&& body) { flat_vectors<4, T, VEC, MASK>(p, j0, j1, body); };
   float m[VEC];   // per component; component c is feature c % d
 #pragma unroll
   for (int c = 0; c < VEC; ++c) m[c] = neg_inf();
@@ -201,22 +194,22 @@ __device__ __forceinline__ void lane_segment(const Params& p, int64_t s, int64_t
 // A wave-class segment in the row mapping reduced by a group of lanes that
 // together hold one row (lane `feature_lane` owns features feature_lane*VEC
 // .. +VEC): every lane walks all rows of the segment on its own, so no lane
-// waits for another; four rows' loads in flight per lane.
+// waits for another; eight rows' loads in flight per lane.
 template <int OP, class T, int VEC, bool MASK>
 __device__ __forceinline__ void group_segment(const Params& p, int64_t s, int64_t start, int64_t end,
                                               int feature_lane) {
   const int64_t d = p.d;
   const int64_t f0 = (int64_t)feature_lane * VEC;
   if (f0 < d) {
+    // Rows past the segment re-read its last row (in cache) instead of
+    // branching around the load, so the eight loads issue back to back.
     auto rows = [&](auto&& body) {
-      for (int64_t r = start; r < end; r += 4) {
-        float x[4][VEC];
+      for (int64_t r = start; r < end; r += 8) {
+        float x[8][VEC];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (r + u < end) load_input<T, VEC, MASK>(p, (r + u) * d + f0, x[u]);
-        }
+        for (int u = 0; u < 8; ++u) load_input<T, VEC, MASK>(p, (r + u < end ? r + u : end - 1) * d + f0, x[u]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 8; ++u) {
           if (r + u < end) body(r + u, x[u]);
         }
       }
@@ -355,6 +348,55 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
 }
 
 // ---------------------------------------------------------------------------
+// Wave-class batches: in the flat mapping 64 segments per wave, one per
+// lane; in the row mapping one per group of the G lanes that hold a row
+// (64 / G per wave), or one per wave when a row needs more than a wave.
+
+template <bool FLAT, int VEC>
+__device__ __forceinline__ int wave_group(int d) {
+  return FLAT ? 1 : (tiles_of<VEC>(d, kWave) == 1 ? lanes_per_row(d, VEC, kWave) : kWave);
+}
+
+template <bool FLAT, int VEC>
+__device__ __forceinline__ int64_t wave_batch_size(int d) {
+  return (int64_t)(kWave / wave_group<FLAT, VEC>(d)) * kWavesPerBlock;
+}
+
+// Batch `index` of the wave class: its segments are queue positions
+// index*batch .. of the first n_wave (every segment in order if `direct`).
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__device__ __forceinline__ void wave_batch(const Params& p, int64_t index, int64_t n_wave, bool direct) {
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1), w = t / kWave;
+  const int tiles_wave = FLAT ? 1 : tiles_of<VEC>(p.d, kWave);
+  const int group = wave_group<FLAT, VEC>(p.d);
+  const int per_wave = kWave / group;
+  // Wave w takes per_wave positions, one per group.
+  const int64_t pos = index * per_wave * kWavesPerBlock + w * per_wave + lane / group;
+  const bool have = pos < n_wave;
+  int64_t s = 0, start = 0, end = 0;
+  if (have) {
+    s = direct ? pos : p.queue[pos];
+    segment_rows<OffT>(p, s, start, end);
+  }
+  // Reduced by its own lane (flat: at most kLaneElems elements) or lane
+  // group (at most kGroupRows rows, when a row needs less than a wave),
+  // else by the whole wave.
+  const bool alone = have && (FLAT ? (end - start) * p.d <= kLaneElems
+                                   : group < kWave && end - start <= kGroupRows);
+  if (alone) {
+    if constexpr (FLAT) lane_segment<OP, T, VEC, MASK>(p, s, start, end);
+    else group_segment<OP, T, VEC, MASK>(p, s, start, end, lane % group);
+  }
+  uint64_t todo = __ballot(have && !alone && lane % group == 0);   // one bit per group
+  while (todo) {
+    const int src = __ffsll((unsigned long long)todo) - 1;
+    todo &= todo - 1;
+    const int64_t ss = __shfl(s, src, kWave);
+    const int64_t a = __shfl(start, src, kWave), b = __shfl(end, src, kWave);
+    for (int tile = 0; tile < tiles_wave; ++tile) process_segment<OP, T, VEC, FLAT, MASK, false>(p, ss, a, b, tile, nullptr);
+  }
+}
 
 template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
@@ -362,17 +404,10 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   __shared__ int64_t ticket_s;
   __shared__ int flag_s;
   const int t = threadIdx.x;
-  const int lane = t & (kWave - 1), w = t / kWave;
   const int tiles_block = FLAT ? 1 : tiles_of<VEC>(p.d, kBlock);
-  const int tiles_wave = FLAT ? 1 : tiles_of<VEC>(p.d, kWave);
   // Ticket order: split parts (x feature tiles), block-class segments,
-  // batches of kWaveBatch wave-class segments.
-  // A wave-class batch: in the flat mapping 64 segments per wave, one per
-  // lane; in the row mapping one per group of the G lanes that hold a row
-  // (64 / G per wave), or one per wave when a row needs more than a wave.
-  const int group = FLAT ? 1 : (tiles_wave == 1 ? lanes_per_row(p.d, VEC, kWave) : kWave);
-  const int per_wave = kWave / group;
-  const int64_t batch = (int64_t)per_wave * kWavesPerBlock;
+  // batches of wave-class segments.
+  const int64_t batch = wave_batch_size<FLAT, VEC>(p.d);
   // Short-segment schedule: every segment, in order, is wave class; no
   // counters, grid-stride batches.
   const bool direct = p.short_segments != 0;
@@ -403,30 +438,7 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
       // (process_segment counts a visit at tile 0 only.)
       for (int tile = 0; tile < tiles_block; ++tile) process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, tile, lds);
     } else {
-      // Wave-class batch: wave w takes per_wave positions, one per group.
-      const int64_t pos = (ticket - n_parts - n_block) * batch + w * per_wave + lane / group;
-      const bool have = pos < n_wave;
-      int64_t s = 0, start = 0, end = 0;
-      if (have) {
-        s = direct ? pos : p.queue[pos];
-        segment_rows<OffT>(p, s, start, end);
-      }
-      // Reduced by its own lane / group when short (elements per lane at
-      // most kLaneElems), else by the whole wave.
-      const bool alone = have && (FLAT ? (end - start) * p.d : (end - start) * group) <= kLaneElems &&
-                         (FLAT || tiles_wave == 1);
-      if (alone) {
-        if constexpr (FLAT) lane_segment<OP, T, VEC, MASK>(p, s, start, end);
-        else group_segment<OP, T, VEC, MASK>(p, s, start, end, lane % group);
-      }
-      uint64_t todo = __ballot(have && !alone && lane % group == 0);   // one bit per group
-      while (todo) {
-        const int src = __ffsll((unsigned long long)todo) - 1;
-        todo &= todo - 1;
-        const int64_t ss = __shfl(s, src, kWave);
-        const int64_t a = __shfl(start, src, kWave), b = __shfl(end, src, kWave);
-        for (int tile = 0; tile < tiles_wave; ++tile) process_segment<OP, T, VEC, FLAT, MASK, false>(p, ss, a, b, tile, nullptr);
-      }
+      wave_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - n_parts - n_block, n_wave, direct);
     }
   }
 }

@@ -146,7 +146,8 @@ def measure(cases: list[Case], out: Path, *, log=print) -> int:
                 run = lambda: program.run(x, off, y, select=schedule, max_len=max_len)   # noqa: E731
                 run()
                 times[schedule] = round(_time_calls(torch, run), 2)
-            record = {**asdict(case), "key": case.key, "max_len": max_len, "us": times}
+            record = {**asdict(case), "key": case.key, "max_len": max_len, "fused": bool(program.metadata["fused"]),
+                      "us": times}
             sink.write(json.dumps(record) + "\n")
             sink.flush()
             measured += 1
@@ -160,6 +161,10 @@ def measure(cases: list[Case], out: Path, *, log=print) -> int:
 
 def load(path: Path) -> list[dict]:
     return [json.loads(line) for line in Path(path).read_text().splitlines() if line.strip()]
+
+
+def _family(record: dict) -> str:
+    return family(record["op"], bool(record.get("fused", False)))
 
 
 def _row(record: dict) -> np.ndarray:
@@ -215,7 +220,8 @@ def choices(model: CostModel, records: list[dict]) -> list[tuple[dict, str]]:
     out = []
     for record in records:
         element = 2 if record["dtype"] == "bf16" else 4
-        chosen, _ = model.choose(record["op"], record["n"], record["b"], record["d"], record["max_len"], element)
+        chosen, _ = model.choose(record["op"], record["n"], record["b"], record["d"], record["max_len"], element,
+                                 fused=bool(record.get("fused", False)))
         out.append((record, chosen))
     return out
 
@@ -229,8 +235,8 @@ def evaluate(model: CostModel, records: list[dict]) -> dict:
         best = min(times.values())
         ok = times[chosen] <= best * (1 + WITHIN)
         good += ok
-        per_family[family(record["op"])][0] += ok
-        per_family[family(record["op"])][1] += 1
+        per_family[_family(record)][0] += ok
+        per_family[_family(record)][1] += 1
         if not ok:
             misses.append({"key": record["key"], "chosen": chosen, "us": times,
                            "slowdown": round(times[chosen] / best, 3)})
@@ -243,7 +249,7 @@ def fit(records: list[dict]) -> dict:
     """The cost model file for ``records`` (train measurements)."""
     coefficients, errors = {}, {}
     for name in FAMILIES:
-        subset = [r for r in records if family(r["op"]) == name]
+        subset = [r for r in records if _family(r) == name]
         if len(subset) < TERMS:
             raise ValueError(f"too few {name} measurements to fit ({len(subset)})")
         coefficients[name], errors[name] = {}, {}

@@ -105,7 +105,8 @@ class CompiledProgram:
                 self._choices.clear()
             element = 2 if self.spec.dtype == "bf16" else 4
             choice = self._choices[key] = default_model().choose(self.spec.op, n, b, self.spec.feature_dim, max_len,
-                                                                 element, l2_mib=l2_mib)
+                                                                 element, l2_mib=l2_mib,
+                                                                 fused=bool(self._metadata["fused"]))
         return choice
 
     def close(self) -> None:
@@ -274,7 +275,7 @@ class CompiledProgram:
         then one worker launch takes the segments in order (no classify, no
         workspace). A max_len that is too small only costs time."""
         thresholds = self._metadata["thresholds"]
-        return (self._schedule == "classified" and max_len is not None and not self._metadata["fused"]
+        return (self._schedule == "classified" and max_len is not None
                 and not self.spec.debug_visits and bool(thresholds) and 0 < thresholds[0]
                 and max_len <= thresholds[0])
 
@@ -354,6 +355,11 @@ class CompiledProgram:
                     view = workspace[offset:offset + nbytes].view(dtypes[name])
                     if name == "segment_ids":
                         view = view.view(3, b)
+                    if name == "class_counts" and plan.fused:
+                        # The register-resident softmax counts its wave class
+                        # in slot 7; present [wave, block, split] as elsewhere.
+                        view = view.clone()
+                        view[0] = view[7]
                     debug_buffers[name] = view
         return self._report(started, names, grids, int(plan.workspace_bytes), mode=mode, selected=selected,
                             selection=selection, validation_bytes=validation_bytes, validation_ms=validation_ms)

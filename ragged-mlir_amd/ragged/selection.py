@@ -3,9 +3,11 @@
 Same decision rule as the reference's ``python/ragged/selection.py``
 (:56-126): predict the complete-call time of each schedule from host-known
 statistics (N, B, D, element size and the caller's longest segment L) with a
-linear model per operation family {reduce, softmax} and schedule, and
-classify only when that is predicted faster by ``margin``; without L keep
-classification.
+linear model per operation family and schedule, and classify only when that
+is predicted faster by ``margin``; without L keep classification. The
+families are the reference's {reduce, softmax} plus ``softmax_fused``: a
+softmax whose classified schedule is the register-resident worker pays a
+per-segment cost the streaming worker does not, so it gets its own fit.
 
 The terms are re-derived for MI355X (model version 3, seven terms, µs):
 
@@ -31,13 +33,15 @@ from .errors import CacheMismatch
 
 MODEL_PATH = Path(__file__).with_name("cost_model.json")
 SCHEDULES = ("classified", "naive")
-FAMILIES = ("reduce", "softmax")
+FAMILIES = ("reduce", "softmax", "softmax_fused")
 TERMS = 7
 VERSION = 3
 
 
-def family(op: str) -> str:
-    return "softmax" if op == "softmax" else "reduce"
+def family(op: str, fused: bool = False) -> str:
+    if op != "softmax":
+        return "reduce"
+    return "softmax_fused" if fused else "softmax"
 
 
 def features(n: int, b: int, d: int, max_len: int, element_bytes: int = 4, op: str = "sum",
@@ -84,20 +88,20 @@ class CostModel:
         return cls.from_dict(json.loads(Path(path).read_text()))
 
     def predict(self, schedule: str, op: str, n: int, b: int, d: int, max_len: int, element_bytes: int = 4,
-                l2_mib: float | None = None) -> float:
+                l2_mib: float | None = None, fused: bool = False) -> float:
         terms = features(n, b, d, max_len, element_bytes, op, self.l2_mib if l2_mib is None else l2_mib,
                          self.mall_mib)
-        return sum(c * x for c, x in zip(self.coefficients[family(op)][schedule], terms))
+        return sum(c * x for c, x in zip(self.coefficients[family(op, fused)][schedule], terms))
 
     def choose(self, op: str, n: int, b: int, d: int, max_len: int | None, element_bytes: int = 4,
-               l2_mib: float | None = None) -> tuple[str, dict[str, Any]]:
+               l2_mib: float | None = None, fused: bool = False) -> tuple[str, dict[str, Any]]:
         """The schedule to run and the inputs and predictions behind it."""
         if max_len is None:
             return "classified", {"max_len": None, "reason": "no length statistics on the host"}
         if l2_mib is not None and not (isinstance(l2_mib, (int, float)) and l2_mib > 0):
             raise ValueError("l2_mib must be a positive capacity in MiB")
-        classified = self.predict("classified", op, n, b, d, max_len, element_bytes, l2_mib)
-        naive = self.predict("naive", op, n, b, d, max_len, element_bytes, l2_mib)
+        classified = self.predict("classified", op, n, b, d, max_len, element_bytes, l2_mib, fused)
+        naive = self.predict("naive", op, n, b, d, max_len, element_bytes, l2_mib, fused)
         selected = "classified" if classified < naive * (1 - self.margin) else "naive"
         return selected, {"max_len": max_len, "l2_mib": self.l2_mib if l2_mib is None else l2_mib,
                           "predicted_us": {"classified": round(classified, 2), "naive": round(naive, 2)}}

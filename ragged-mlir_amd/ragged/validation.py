@@ -37,7 +37,8 @@ def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> 
     """Role names in launch order. The classified schedule runs init,
     classify and one worker over the wave, block and split classes (plus the
     split normalise pass of a softmax); with ``fused`` a softmax runs its
-    register-resident worker plus its re-read pass instead."""
+    register-resident worker, then a pass over the deferred chunks and the
+    wave class."""
     phase = _phase(spec.op)
     if classes == ["block"] and spec.strategy == "naive":
         return [phase]

@@ -14,7 +14,9 @@ from ragged.selection import CostModel, features
 TRUTH = {"reduce": {"classified": [20.0, 0.0, 0.0, 0.5, 0.0, 0.0, 0.0],
                     "naive": [8.0, 0.0, 30.0, 2.0, 0.0, 0.0, 0.0]},
          "softmax": {"classified": [25.0, 0.0, 0.0, 0.8, 0.0, 0.0, 0.0],
-                     "naive": [8.0, 0.0, 60.0, 3.0, 0.0, 0.0, 0.0]}}
+                     "naive": [8.0, 0.0, 60.0, 3.0, 0.0, 0.0, 0.0]},
+         "softmax_fused": {"classified": [25.0, 0.0, 0.0, 12.0, 0.0, 0.0, 0.0],
+                           "naive": [8.0, 0.0, 60.0, 3.0, 0.0, 0.0, 0.0]}}
 
 
 def synthetic_records(cases, truth):
@@ -23,9 +25,10 @@ def synthetic_records(cases, truth):
         # Lengths are not generated here: max_len from the distribution's cap.
         max_len = case.n if case.distribution == "burst" else max(1, case.n // case.b * 8)
         row = np.array(features(case.n, case.b, case.d, max_len, case.element_bytes, case.op))
-        fam = "softmax" if case.op == "softmax" else "reduce"
+        fused = case.op == "softmax" and case.d >= 8
+        fam = ("softmax_fused" if fused else "softmax") if case.op == "softmax" else "reduce"
         us = {s: float(row @ np.array(truth[fam][s])) for s in ("classified", "naive")}
-        records.append({**case.__dict__, "key": case.key, "max_len": max_len, "us": us})
+        records.append({**case.__dict__, "key": case.key, "max_len": max_len, "fused": fused, "us": us})
     return records
 
 
@@ -46,7 +49,8 @@ def test_fit_recovers_known_coefficients():
     for record in records[:20]:
         for schedule in ("classified", "naive"):
             predicted = model.predict(schedule, record["op"], record["n"], record["b"], record["d"],
-                                      record["max_len"], 2 if record["dtype"] == "bf16" else 4)
+                                      record["max_len"], 2 if record["dtype"] == "bf16" else 4,
+                                      fused=record["fused"])
             assert predicted == pytest.approx(record["us"][schedule], rel=1e-3)
     assert calibrate.evaluate(model, records)["share"] == 1.0
 

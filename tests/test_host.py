@@ -56,10 +56,14 @@ def test_abi_version_and_build_info():
                                               ("f32", 1024, 16)])
 def test_register_resident_defaults(dtype, d, capacity):
     """Softmax specs whose rows fit one workgroup's registers default to the
-    register-resident schedule, with one chunk = the workgroup's capacity."""
+    register-resident schedule, with one chunk = the workgroup's capacity;
+    the wave class keeps the streaming worker's threshold, below the block
+    class."""
     spec = native.make_spec("softmax", dtype, "i64", d)
     assert native.uses_fused(spec)
-    assert spec.part_rows == capacity and spec.t_block == capacity and spec.t_wave == 0
+    assert spec.part_rows == capacity and spec.t_block == capacity
+    streaming = native.make_spec("sum", dtype, "i64", d)
+    assert spec.t_wave == min(streaming.t_wave, capacity - 1) and 0 < spec.t_wave < spec.t_block
 
 
 def test_reductions_keep_the_class_pipeline():
