@@ -121,7 +121,8 @@ typedef struct rg_plan {
 enum rg_buffer {
   RG_BUF_COUNTERS = 0,      /* i64[8] wave/block/split counts, split items, work ticket, deferred
                                count, tree items; slot 7: the wave count of a register-resident
-                               softmax (whose slot 0 stays 0) */
+                               softmax (whose slot 0 stays 0); then 16 ticket counters of the
+                               classified worker, 256 bytes apart (4352 bytes in all) */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class */
   RG_BUF_ITEM_POS = 2,      /* i64[items_cap] split position of each item */
   RG_BUF_PART_BEGIN = 3,    /* i64[B_split] first item of each split segment */

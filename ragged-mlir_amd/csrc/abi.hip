@@ -442,7 +442,7 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   int64_t stat_bytes, item_bytes;
   if (!mul_ok(items_cap, (int64_t)d * 4, &item_bytes) || !mul_ok(b_split, (int64_t)d * 4, &stat_bytes))
     return fail(RG_E_INVALID, "split workspace bytes overflow");
-  sizes[RG_BUF_COUNTERS] = 8 * 8;
+  sizes[RG_BUF_COUNTERS] = (int64_t)rg::kTicketStride * 8 * (1 + rg::kTicketLanes);
   if (!module->fused) {
     // Part arrivals per split segment (the worker's last part combines).
     if (!mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE])) return fail(RG_E_INVALID, "arrival bytes overflow");

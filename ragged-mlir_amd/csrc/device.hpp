@@ -38,6 +38,12 @@ constexpr int kUnroll = 4;             // rows (or flat vectors) loaded per lane
 constexpr int kCombineFeatures = 64;   // consecutive features per split-combine pass
 constexpr int kLaneElems = 64;         // classified worker: flat elements one lane reduces alone
 constexpr int kGroupRows = 32;         // classified worker: rows one lane group walks alone
+// The classified worker's work tickets come from kTicketLanes counters,
+// kTicketStride i64 (256 bytes) apart after the eight class counters:
+// atomics on one address serialise at about 12.5 ns each on MI355X, on 16
+// addresses at about 1 ns per ticket.
+constexpr int kTicketLanes = 16;
+constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
@@ -76,7 +82,8 @@ struct Params {
   int64_t b_split;         // capacity of the split queue / statistics rows
   int64_t* counters;       // [8]: wave, block, split segment counts; split items;
                            //      work ticket; deferred chunks; tree items; wave
-                           //      count of a register-resident softmax
+                           //      count of a register-resident softmax; then
+                           //      the worker's ticket lanes (kTicketStride apart)
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item
   int64_t* part_begin;     // [B] first item of each split-queue position

@@ -403,6 +403,7 @@ __global__ __launch_bounds__(kBlock) void k_init(Params p) {
   const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t threads = (int64_t)gridDim.x * kBlock;
   if (tid < 8) p.counters[tid] = 0;
+  if (tid < kTicketLanes) p.counters[kTicketStride * (1 + tid)] = 0;
   if (p.visits) {
     for (int64_t s = tid; s < p.b; s += threads) p.visits[s] = 0;
   }

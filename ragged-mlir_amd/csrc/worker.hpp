@@ -417,12 +417,17 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int64_t n_wave = direct ? p.b : p.counters[0];
   const int64_t n_batches = (n_wave + batch - 1) / batch;
   const int64_t total = n_parts + n_block + n_batches;
+  // Tickets interleave over the lanes: lane k hands out k, k + lanes, ...
+  // to the workgroups blockIdx = k (mod lanes), every lane has at least one.
+  const int lanes = gridDim.x < kTicketLanes ? (int)gridDim.x : kTicketLanes;
+  const int lane_id = (int)(blockIdx.x % lanes);
+  unsigned long long* counter = (unsigned long long*)(p.counters + kTicketStride * (1 + lane_id));
   int64_t next = blockIdx.x;
   for (;;) {
     int64_t ticket = next;
     if (!direct) {
       __syncthreads();
-      if (t == 0) ticket_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+      if (t == 0) ticket_s = (int64_t)atomicAdd(counter, 1ull) * lanes + lane_id;
       __syncthreads();
       ticket = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)ticket_s >> 32)) << 32) |
                          __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)ticket_s));

@@ -355,6 +355,8 @@ class CompiledProgram:
                     view = workspace[offset:offset + nbytes].view(dtypes[name])
                     if name == "segment_ids":
                         view = view.view(3, b)
+                    if name == "class_counts":
+                        view = view[:8]    # the ticket counters follow
                     if name == "class_counts" and plan.fused:
                         # The register-resident softmax counts its wave class
                         # in slot 7; present [wave, block, split] as elsewhere.
