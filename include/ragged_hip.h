@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RG_ABI_VERSION 1
+#define RG_ABI_VERSION 2
 
 enum rg_status {
   RG_OK = 0,
@@ -41,11 +41,11 @@ enum rg_status {
 enum rg_op { RG_OP_SUM = 0, RG_OP_MAX = 1, RG_OP_SOFTMAX = 2 };
 enum rg_dtype { RG_F32 = 0, RG_BF16 = 1 };
 enum rg_index { RG_I32 = 0, RG_I64 = 1 };
-/* RG_SHORT_SEGMENTS: every segment is expected to be at most t_wave rows
- * (the caller's max_len says so): one worker launch takes the segments in
- * order, with no classification and no workspace. Any input is still
+/* RG_SHORT_SEGMENTS: every segment is expected to be at most alone_rows
+ * rows (the caller's max_len says so): one worker launch takes the segments
+ * in order, with no classification and no workspace. Any input is still
  * computed exactly; a longer segment only runs slower. Not available when
- * t_wave is 0. */
+ * alone_rows or t_wave is 0. */
 enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1, RG_SHORT_SEGMENTS = 2 };
 
 /* Kernel roles, in launch order of the classified schedule. */
@@ -81,6 +81,10 @@ typedef struct rg_spec {
   int64_t t_wave;         /* wave class: segments of at most t_wave rows; <0: default */
   int64_t t_block;        /* block class: at most t_block rows; <0: default */
   int64_t part_rows;      /* rows per split part; <0: default */
+  int64_t alone_rows;     /* output of rg_spec_defaults: wave-class segments of at most this
+                             many rows are reduced by one lane (flat mapping) or one group of
+                             the lanes that hold a row (rows narrower than half a wave); the
+                             rest of the wave class by one wave each */
 } rg_spec;
 
 /* Device facts the host cost model and grids use. */
@@ -119,11 +123,15 @@ typedef struct rg_plan {
 
 /* Workspace buffer indices (rg_plan.buffer_offset / buffer_bytes). */
 enum rg_buffer {
-  RG_BUF_COUNTERS = 0,      /* i64[8] wave/block/split counts, split items, work ticket, deferred
-                               count, tree items; slot 7: the wave count of a register-resident
-                               softmax (whose slot 0 stays 0); then 16 ticket counters of the
-                               classified worker, 256 bytes apart (4352 bytes in all) */
-  RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class */
+  RG_BUF_COUNTERS = 0,      /* i64 slots: 0 wave-class segments of at most alone_rows rows, 1 block,
+                               2 split counts, 3 split items, 4 work ticket, 5 deferred count,
+                               6 tree items; 7 slot 0's count for a register-resident softmax
+                               (whose slot 0 stays 0); 8 the rest of the wave class; then 16
+                               ticket counters of the classified worker, 256 bytes apart from
+                               byte 256 (4352 bytes in all) */
+  RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class; the wave class holds
+                               its segments of at most alone_rows rows from the front and the
+                               others from the back */
   RG_BUF_ITEM_POS = 2,      /* i64[items_cap] split position of each item */
   RG_BUF_PART_BEGIN = 3,    /* i64[B_split] first item of each split segment */
   RG_BUF_PARTIALS = 4,      /* f32[items_cap, D] */

@@ -171,16 +171,14 @@ int rg_spec_defaults(rg_spec* spec) {
   const int64_t row = (int64_t)spec->feature_dim * element_bytes(spec->dtype);
   const bool default_wave = spec->t_wave < 0;
   const Geometry geo = choose_geometry(spec->dtype, spec->feature_dim, spec->vectorize != 0);
-  // Wave class: the segments one lane (flat mapping, D below the vector
-  // width) or one group of a row's lanes (row mapping, rows narrower than a
-  // wave) reduces on its own; with rows as wide as a wave, what one wave
-  // reads in one pass.
-  if (default_wave) {
-    const int64_t lanes = (spec->feature_dim + geo.vec - 1) / geo.vec;
-    spec->t_wave = geo.flat ? std::max<int64_t>(1, rg::kLaneElems / spec->feature_dim)
-                 : lanes < rg::kWave ? rg::kGroupRows
-                                     : std::max<int64_t>(1, kWaveBytes / row);
-  }
+  // Segments one lane (flat mapping, D below the vector width) or one group
+  // of the lanes that hold a row (rows of at most half a wave's lanes)
+  // reduces on its own; the wave class adds those one wave reads in one
+  // pass (kWaveBytes).
+  const int64_t lanes = (spec->feature_dim + geo.vec - 1) / geo.vec;
+  spec->alone_rows = geo.flat ? std::max<int64_t>(1, rg::kLaneElems / spec->feature_dim)
+                   : lanes <= rg::kWave / 2 ? rg::kGroupRows : 0;
+  if (default_wave) spec->t_wave = std::max<int64_t>({1, spec->alone_rows, kWaveBytes / row});
   // Softmax with a register-resident worker: a block-class segment and a
   // split chunk are exactly what one workgroup holds in registers.
   const int64_t capacity = spec->op == RG_OP_SOFTMAX
@@ -381,7 +379,7 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   if (b == 0 && n != 0) return fail(RG_E_INVALID, "B=0 requires N=0");
   if (schedule != RG_CLASSIFIED && schedule != RG_BLOCK_PER_SEGMENT && schedule != RG_SHORT_SEGMENTS)
     return fail(RG_E_INVALID, "unknown schedule");
-  if (schedule == RG_SHORT_SEGMENTS && module->spec.t_wave < 1)
+  if (schedule == RG_SHORT_SEGMENTS && (module->spec.t_wave < 1 || module->spec.alone_rows < 1))
     return fail(RG_E_INVALID, "this specialisation has no short-segment schedule");
   if (schedule == RG_BLOCK_PER_SEGMENT && module->spec.debug_visits)
     return fail(RG_E_INVALID, "debug visits require the classified schedule");
@@ -534,6 +532,7 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
     return plan->buffer_bytes[index] ? base + plan->buffer_offset[index] : nullptr;
   };
   p.short_segments = plan->schedule == RG_SHORT_SEGMENTS ? 1 : 0;
+  p.alone_rows = spec.alone_rows;
   if (plan->schedule == RG_CLASSIFIED) {
     p.counters = static_cast<int64_t*>(buffer(RG_BUF_COUNTERS));
     p.queue = static_cast<int64_t*>(buffer(RG_BUF_QUEUE));

@@ -106,6 +106,7 @@ struct Params {
   int64_t* status;         // [7] checked-offsets status
   int64_t min_len, max_len;  // checked-offsets hints, -1 when absent
   int32_t short_segments;  // worker: every segment in order as wave class (no queues)
+  int64_t alone_rows;      // wave-class segments a lane / lane group reduces alone
 };
 
 // ---------------------------------------------------------------------------

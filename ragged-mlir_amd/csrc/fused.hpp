@@ -623,6 +623,9 @@ __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
     if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     __syncthreads();
   }
+  const int64_t n_coop = p.counters[8];
+  for (int64_t i = blockIdx.x; i * kWavesPerBlock < n_coop; i += gridDim.x)
+    coop_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_coop);
   const int64_t n_wave = p.counters[7];
   const int64_t batch = wave_batch_size<false, VEC>(p.d);
   for (int64_t i = blockIdx.x; i * batch < n_wave; i += gridDim.x)

@@ -402,7 +402,8 @@ __global__ __launch_bounds__(kBlock) void k_split_normalize(Params p) {
 __global__ __launch_bounds__(kBlock) void k_init(Params p) {
   const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t threads = (int64_t)gridDim.x * kBlock;
-  if (tid < 8) p.counters[tid] = 0;
+  // Every class counter slot (the first kTicketStride) and every ticket lane.
+  if (tid < kTicketStride) p.counters[tid] = 0;
   if (tid < kTicketLanes) p.counters[kTicketStride * (1 + tid)] = 0;
   if (p.visits) {
     for (int64_t s = tid; s < p.b; s += threads) p.visits[s] = 0;
@@ -434,7 +435,10 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
     segment_rows<OffT>(p, s, start, end);
     length = end - start;
   }
-  const int cls = length <= p.t_wave ? 0 : (length <= p.t_block ? 1 : 2);
+  // Run 0: wave-class segments one lane / lane group reduces alone (front
+  // of the wave queue); run 3: the rest of the wave class, one wave each
+  // (back of the wave queue); runs 1, 2: block and split classes.
+  const int cls = length <= p.t_wave ? (length <= p.alone_rows ? 0 : 3) : (length <= p.t_block ? 1 : 2);
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
   // Queue runs: the workgroup reserves each class's run with one atomic
   // (not one per wave: every wave of the grid adding to the same three
@@ -442,23 +446,24 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
   // of the run in wave order, so a wave's (and the workgroup's) segments of
   // one class sit in consecutive positions in segment order
   // (classified-abi.md:56-66).
-  __shared__ long long run_s[3][kWavesPerBlock];
+  __shared__ long long run_s[4][kWavesPerBlock];
   const int wave = threadIdx.x / kWave;
-  uint64_t ballots[3];
+  uint64_t ballots[4];
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
+  for (int c = 0; c < 4; ++c) {
     ballots[c] = __ballot(active && cls == c);
     if (lane == 0) run_s[c][wave] = (long long)__popcll(ballots[c]);
   }
   __syncthreads();
-  if (threadIdx.x < 3) {
+  if (threadIdx.x < 4) {
     const int c = threadIdx.x;
     long long total = 0;
     for (int w = 0; w < kWavesPerBlock; ++w) total += run_s[c][w];
-    // A register-resident softmax (block_items set) counts its wave class
-    // in counters[7]: k_softmax_deferred takes it, and k_softmax_fused,
-    // which reads counters[0], sees none.
-    const int slot = c == 0 && p.block_items ? 7 : c;
+    // Run 3 is counted in counters[8]. A register-resident softmax
+    // (block_items set) counts run 0 in counters[7]: k_softmax_deferred
+    // takes the wave class, and k_softmax_fused, which reads counters[0],
+    // sees none.
+    const int slot = c == 3 ? 8 : c == 0 && p.block_items ? 7 : c;
     long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + slot), (unsigned long long)total) : 0;
     for (int w = 0; w < kWavesPerBlock; ++w) {
       const long long count = run_s[c][w];
@@ -468,12 +473,12 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
   }
   __syncthreads();
 #pragma unroll
-  for (int c = 0; c < 3; ++c) {
+  for (int c = 0; c < 4; ++c) {
     const bool mine = active && cls == c;
     const uint64_t ballot = ballots[c];
     if (ballot == 0) continue;
     const int64_t pos = run_s[c][wave] + __popcll(ballot & below);
-    if (mine) p.queue[c * p.b + pos] = s;
+    if (mine) p.queue[c == 3 ? p.b - 1 - pos : c * p.b + pos] = s;
     // Register-resident softmax: whole block-class segments are items too.
     if (mine && c == 1 && p.block_items) p.block_items[pos] = Item{start, s, (int32_t)length, -1, 0, 1};
     if (c != 2) continue;

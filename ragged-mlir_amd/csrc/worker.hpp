@@ -362,7 +362,7 @@ __device__ __forceinline__ int64_t wave_batch_size(int d) {
   return (int64_t)(kWave / wave_group<FLAT, VEC>(d)) * kWavesPerBlock;
 }
 
-// Batch `index` of the wave class: its segments are queue positions
+// Batch `index` of the wave-class segments reduced alone: queue positions
 // index*batch .. of the first n_wave (every segment in order if `direct`).
 template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
 __device__ __forceinline__ void wave_batch(const Params& p, int64_t index, int64_t n_wave, bool direct) {
@@ -379,11 +379,10 @@ __device__ __forceinline__ void wave_batch(const Params& p, int64_t index, int64
     s = direct ? pos : p.queue[pos];
     segment_rows<OffT>(p, s, start, end);
   }
-  // Reduced by its own lane (flat: at most kLaneElems elements) or lane
-  // group (at most kGroupRows rows, when a row needs less than a wave),
-  // else by the whole wave.
-  const bool alone = have && (FLAT ? (end - start) * p.d <= kLaneElems
-                                   : group < kWave && end - start <= kGroupRows);
+  // Reduced by its own lane (flat mapping) or lane group (rows narrower
+  // than a wave) when at most alone_rows long, else by the whole wave (only
+  // `direct` batches hold such segments: k_classify queues them apart).
+  const bool alone = have && (FLAT || group < kWave) && end - start <= p.alone_rows;
   if (alone) {
     if constexpr (FLAT) lane_segment<OP, T, VEC, MASK>(p, s, start, end);
     else group_segment<OP, T, VEC, MASK>(p, s, start, end, lane % group);
@@ -398,6 +397,20 @@ __device__ __forceinline__ void wave_batch(const Params& p, int64_t index, int64
   }
 }
 
+// Batch `index` of the rest of the wave class (queued from the back, n_coop
+// segments): one segment per wave, reduced by the whole wave.
+template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
+__device__ __forceinline__ void coop_batch(const Params& p, int64_t index, int64_t n_coop) {
+  const int w = threadIdx.x / kWave;
+  const int64_t pos = index * kWavesPerBlock + w;
+  if (pos >= n_coop) return;
+  const int64_t s = p.queue[p.b - 1 - pos];
+  int64_t start, end;
+  segment_rows<OffT>(p, s, start, end);
+  const int tiles_wave = FLAT ? 1 : tiles_of<VEC>(p.d, kWave);
+  for (int tile = 0; tile < tiles_wave; ++tile) process_segment<OP, T, VEC, FLAT, MASK, false>(p, s, start, end, tile, nullptr);
+}
+
 template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   __shared__ float lds[kBlock * VEC * 2];
@@ -406,7 +419,8 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int t = threadIdx.x;
   const int tiles_block = FLAT ? 1 : tiles_of<VEC>(p.d, kBlock);
   // Ticket order: split parts (x feature tiles), block-class segments,
-  // batches of wave-class segments.
+  // wave-class segments one per wave, batches of wave-class segments
+  // reduced alone.
   const int64_t batch = wave_batch_size<FLAT, VEC>(p.d);
   // Short-segment schedule: every segment, in order, is wave class; no
   // counters, grid-stride batches.
@@ -414,9 +428,12 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int64_t n_items = direct ? 0 : (p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap);
   const int64_t n_parts = n_items * tiles_block;
   const int64_t n_block = direct ? 0 : p.counters[1];
+  const int64_t n_coop = direct ? 0 : p.counters[8];
+  const int64_t n_coop_batches = (n_coop + kWavesPerBlock - 1) / kWavesPerBlock;
   const int64_t n_wave = direct ? p.b : p.counters[0];
   const int64_t n_batches = (n_wave + batch - 1) / batch;
-  const int64_t total = n_parts + n_block + n_batches;
+  const int64_t before_alone = n_parts + n_block + n_coop_batches;
+  const int64_t total = before_alone + n_batches;
   // Tickets interleave over the lanes: lane k hands out k, k + lanes, ...
   // to the workgroups blockIdx = k (mod lanes), every lane has at least one.
   const int lanes = gridDim.x < kTicketLanes ? (int)gridDim.x : kTicketLanes;
@@ -442,8 +459,10 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
       segment_rows<OffT>(p, s, start, end);
       // (process_segment counts a visit at tile 0 only.)
       for (int tile = 0; tile < tiles_block; ++tile) process_segment<OP, T, VEC, FLAT, MASK, true>(p, s, start, end, tile, lds);
+    } else if (ticket < before_alone) {
+      coop_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - n_parts - n_block, n_coop);
     } else {
-      wave_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - n_parts - n_block, n_wave, direct);
+      wave_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - before_alone, n_wave, direct);
     }
   }
 }

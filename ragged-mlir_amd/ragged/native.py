@@ -17,7 +17,7 @@ import threading
 from .errors import RuntimeUnavailable, ValidationError
 
 LIBRARY_PATH = Path(__file__).with_name("libragged_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OPS = {"sum": 0, "max": 1, "softmax": 2}
 DTYPES = {"f32": 0, "bf16": 1}
@@ -37,7 +37,7 @@ class Spec(ctypes.Structure):
     _fields_ = [("op", ctypes.c_int32), ("dtype", ctypes.c_int32), ("offsets_dtype", ctypes.c_int32),
                 ("feature_dim", ctypes.c_int32), ("scale", ctypes.c_float), ("has_mask", ctypes.c_int32),
                 ("vectorize", ctypes.c_int32), ("debug_visits", ctypes.c_int32), ("t_wave", ctypes.c_int64),
-                ("t_block", ctypes.c_int64), ("part_rows", ctypes.c_int64)]
+                ("t_block", ctypes.c_int64), ("part_rows", ctypes.c_int64), ("alone_rows", ctypes.c_int64)]
 
 
 class DeviceProps(ctypes.Structure):
@@ -149,7 +149,7 @@ def make_spec(op: str, dtype: str, offsets_dtype: str, feature_dim: int, *, scal
               mask: bool = False, vectorize: bool = True, debug_visits: bool = False,
               t_wave: int = -1, t_block: int = -1, part_rows: int = -1) -> Spec:
     spec = Spec(OPS[op], DTYPES[dtype], INDEX_DTYPES[offsets_dtype], feature_dim, scale, int(mask),
-                int(vectorize), int(debug_visits), t_wave, t_block, part_rows)
+                int(vectorize), int(debug_visits), t_wave, t_block, part_rows, 0)
     _check(library().rg_spec_defaults(ctypes.byref(spec)), "rg_spec_defaults")
     return spec
 

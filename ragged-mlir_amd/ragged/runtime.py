@@ -270,14 +270,15 @@ class CompiledProgram:
             optimizations=metadata["optimizations"], d_tile=metadata["d_tile"], d_vector=metadata["d_vector"],
             resources=None, streams=1, selected=selected, selection=selection)
 
-    def _short_segments(self, max_len: int | None) -> bool:
-        """Whether the caller's max_len puts every segment in the wave class:
-        then one worker launch takes the segments in order (no classify, no
-        workspace). A max_len that is too small only costs time."""
+    def _short_segments(self, module: native.NativeModule, max_len: int | None) -> bool:
+        """Whether the caller's max_len lets one lane (or lane group) reduce
+        every segment alone: then one worker launch takes the segments in
+        order (no classify, no workspace). A max_len that is too small only
+        costs time."""
         thresholds = self._metadata["thresholds"]
         return (self._schedule == "classified" and max_len is not None
                 and not self.spec.debug_visits and bool(thresholds) and 0 < thresholds[0]
-                and max_len <= thresholds[0])
+                and 0 < module.spec.alone_rows and max_len <= module.spec.alone_rows)
 
     def _run(self, values, offsets, out, stream, mode, *, debug_buffers, mask, selected, selection,
              max_len: int | None = None) -> ExecutionReport:
@@ -326,7 +327,7 @@ class CompiledProgram:
                 if b == 0:
                     return self._report(started, names, grids, 0, mode=mode, selected=selected, selection=selection,
                                         validation_bytes=validation_bytes, validation_ms=validation_ms)
-            short = self._short_segments(max_len)
+            short = self._short_segments(module, max_len)
             if short:
                 selection = {**selection, "short_segments": True}
             plan = self._plan(module, n, b, "short" if short else self._schedule)
@@ -355,14 +356,26 @@ class CompiledProgram:
                     view = workspace[offset:offset + nbytes].view(dtypes[name])
                     if name == "segment_ids":
                         view = view.view(3, b)
-                    if name == "class_counts":
-                        view = view[:8]    # the ticket counters follow
-                    if name == "class_counts" and plan.fused:
-                        # The register-resident softmax counts its wave class
-                        # in slot 7; present [wave, block, split] as elsewhere.
-                        view = view.clone()
-                        view[0] = view[7]
                     debug_buffers[name] = view
+                # Present the wave class as one count and one run of ids: the
+                # library counts the segments reduced alone in slot 0 (slot
+                # 7 for a register-resident softmax) and queues them from the
+                # front, the others in slot 8 and from the back. The copies
+                # are ordered after the launch on its stream; reading the
+                # counts makes a debug call synchronise.
+                if "class_counts" in debug_buffers:
+                    with torch.cuda.stream(active):
+                        counts = debug_buffers["class_counts"]
+                        alone = counts[7 if plan.fused else 0]
+                        coop = counts[8]
+                        debug_buffers["class_counts"] = presented = counts[:8].clone()
+                        presented[0] = alone + coop
+                        if "segment_ids" in debug_buffers:
+                            ids = debug_buffers["segment_ids"].clone()
+                            n_alone, n_coop = int(alone), int(coop)
+                            if n_coop:
+                                ids[0, n_alone:n_alone + n_coop] = debug_buffers["segment_ids"][0, b - n_coop:]
+                            debug_buffers["segment_ids"] = ids
         return self._report(started, names, grids, int(plan.workspace_bytes), mode=mode, selected=selected,
                             selection=selection, validation_bytes=validation_bytes, validation_ms=validation_ms)
 

@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 if not torch.cuda.is_available():  # pragma: no cover - CPU containers
     pytest.skip("no ROCm device", allow_module_level=True)
 
-from ragged import Compiler, Hints, Optimizations, ProgramSpec  # noqa: E402
+from ragged import Compiler, Hints, Optimizations, ProgramSpec, native  # noqa: E402
 from ragged.workloads import make_lengths, offsets_from_lengths  # noqa: E402
 
 _programs = {}
@@ -186,11 +186,13 @@ def test_unvectorized_unaligned_views(artifact_cache):
 @pytest.mark.parametrize("op", OPS)
 @pytest.mark.parametrize("d,dtype", [(1, "f32"), (2, "f32"), (4, "bf16"), (3, "f32"), (128, "f32"), (8, "bf16")])
 def test_short_segment_schedule(artifact_cache, op, d, dtype):
-    """With max_len at most the wave threshold one worker launch takes the
-    segments in order; a max_len below the true longest segment (a caller's
-    mistake) still gives exact results."""
+    """With max_len at most alone_rows (segments one lane or lane group
+    reduces alone) one worker launch takes the segments in order; a max_len
+    below the true longest segment (a caller's mistake) still gives exact
+    results."""
     program = program_for(artifact_cache, op, dtype, d, "i64")
-    t_wave = program.metadata["thresholds"][0]
+    t_wave = native.make_spec(op, dtype, "i64", d).alone_rows
+    assert t_wave > 0
     rng = np.random.default_rng(40 + d)
     lengths = rng.integers(0, t_wave + 1, size=3000).astype(np.int64)
     lengths[::7] = 0
@@ -208,3 +210,69 @@ def test_short_segment_schedule(artifact_cache, op, d, dtype):
     actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified", max_len=t_wave)
     assert report.selection.get("short_segments")
     check(actual, values, offsets, op=op, dtype=dtype)
+
+
+@pytest.mark.parametrize("d,dtype", [(1, "f32"), (2, "bf16"), (4, "f32"), (3, "f32"), (32, "bf16"), (128, "f32"),
+                                     (96, "f32"), (1024, "f32")])
+@pytest.mark.parametrize("op", OPS)
+def test_wave_class_runs(artifact_cache, op, d, dtype):
+    """The wave class in its two runs: segments of at most alone_rows rows
+    (one lane or lane group each, queued from the front) and the rest up to
+    t_wave (one wave each, queued from the back), mixed with block and split
+    segments and empties; exact results, and the debug view presents the
+    wave class as one run (reference test_classified.py:102-143)."""
+    spec = native.make_spec(op, dtype, "i64", d)
+    alone, t_wave, t_block = spec.alone_rows, spec.t_wave, spec.t_block
+    assert alone <= t_wave < t_block
+    rng = np.random.default_rng(900 + d)
+    pieces = [np.zeros(40, dtype=np.int64), rng.integers(1, max(alone, 1) + 1, size=300),
+              rng.integers(alone + 1, t_wave + 1, size=300) if t_wave > alone else np.zeros(0, np.int64),
+              np.array([t_wave, t_wave + 1, alone, alone + 1, t_block, t_block + 1]),
+              rng.integers(t_wave + 1, min(t_block, t_wave + 4000) + 1, size=20)]
+    lengths = rng.permutation(np.concatenate(pieces)).astype(np.int64)
+    lengths = np.maximum(lengths, 0)
+    budget = 3_000_000 // d
+    while lengths.sum() > budget:     # keep the oracle quick: shorten the longest
+        lengths[np.argmax(lengths)] //= 2
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    program = program_for(artifact_cache, op, dtype, d, "i64")
+    actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified")
+    assert report.selected == "classified"
+    check(actual, values, offsets, op=op, dtype=dtype)
+    debug = program_for(artifact_cache, op, dtype, d, "i64", debug_visits=True)
+    buffers = {}
+    actual, _ = run_program(debug, values, offsets, dtype=dtype, op=op, debug_buffers=buffers)
+    check(actual, values, offsets, op=op, dtype=dtype)
+    thresholds = debug.metadata["thresholds"]
+    classes = np.where(lengths <= thresholds[0], 0, np.where(lengths <= thresholds[1], 1, 2))
+    counts = buffers["class_counts"].cpu().numpy()
+    np.testing.assert_array_equal(counts[:3], np.bincount(classes, minlength=3))
+    ids = buffers["segment_ids"].cpu().numpy()
+    for c in range(3):
+        np.testing.assert_array_equal(np.sort(ids[c, :counts[c]]), np.flatnonzero(classes == c))
+    np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
+
+
+@pytest.mark.parametrize("op,dtype,d", [("sum", "f32", 1), ("max", "f32", 128), ("softmax", "f32", 1024),
+                                        ("softmax", "bf16", 128), ("softmax", "f32", 2), ("sum", "bf16", 1024)])
+def test_workspace_contents_do_not_matter(artifact_cache, op, dtype, d):
+    """Every counter, queue and table a kernel reads is written by the
+    library in the same call: a reused workspace full of 0xFF bytes gives
+    the same exact results (regression: a class counter the init kernel
+    did not clear)."""
+    rng = np.random.default_rng(77 + d)
+    lengths = np.concatenate([np.zeros(30, np.int64), rng.integers(1, 40, size=400),
+                              rng.integers(100, 3000, size=12), [20000 // d + 700]])
+    lengths = rng.permutation(lengths).astype(np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    program = program_for(artifact_cache, op, dtype, d, "i64")
+    for _ in range(2):
+        actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified")
+        assert report.workspace_bytes > 0
+        check(actual, values, offsets, op=op, dtype=dtype)
+        torch.cuda.synchronize()
+        for workspace in program._workspaces.values():
+            workspace.fill_(255)
+        torch.cuda.synchronize()

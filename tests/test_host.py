@@ -66,6 +66,18 @@ def test_register_resident_defaults(dtype, d, capacity):
     assert spec.t_wave == min(streaming.t_wave, capacity - 1) and 0 < spec.t_wave < spec.t_block
 
 
+@pytest.mark.parametrize("d,dtype,alone", [(1, "f32", 64), (2, "f32", 32), (4, "bf16", 16), (3, "f32", 32),
+                                           (128, "f32", 32), (256, "bf16", 32), (192, "f32", 0), (1024, "f32", 0)])
+def test_alone_rows(d, dtype, alone):
+    """Wave-class segments one lane (flat: kLaneElems elements) or one lane
+    group (rows of at most 32 vectors: 32 rows) reduces alone; the wave class
+    reaches at least as far, and at least 8 KiB of rows."""
+    spec = native.make_spec("sum", dtype, "i64", d)
+    assert spec.alone_rows == alone
+    row = d * (2 if dtype == "bf16" else 4)
+    assert spec.t_wave == max(1, alone, 8192 // row) < spec.t_block
+
+
 def test_reductions_keep_the_class_pipeline():
     for op in ("sum", "max"):
         spec = native.make_spec(op, "f32", "i64", 128)
