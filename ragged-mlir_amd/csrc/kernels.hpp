@@ -115,6 +115,19 @@ __device__ __forceinline__ void normalize_rows(const Params& p, const RowGeo& g,
 
 // ---------------------------------------------------------------------------
 // FLAT mapping traversal of elements [lo, hi) (= rows [r0, r1) times D).
+
+// The elements of vector j one by one, each index clamped into [lo, hi)
+// (lo < hi): no load leaves the segment, and with no branch between them
+// the VEC loads are in flight together. Components outside [lo, hi) hold
+// a copy of an element inside; callers mask them.
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void load_partial(const Params& p, int64_t j, int64_t lo, int64_t hi, float (&x)[VEC]) {
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    const int64_t e = j * VEC + c;
+    x[c] = load_input1<T, MASK>(p, e < lo ? lo : (e < hi ? e : hi - 1));
+  }
+}
 // Vector j covers elements [j*VEC, j*VEC + VEC); component c is feature c % D.
 
 template <int OP, class T, int VEC, bool MASK>
@@ -128,10 +141,12 @@ __device__ __forceinline__ void fold_flat(const Params& p, int g, int t, int64_t
   const bool tail_partial = hi % VEC != 0 && tail != head;
   if ((head_partial && t == 0) || (tail_partial && t == 1)) {
     const int64_t j = t == 0 ? head : tail;
+    float x[VEC];
+    load_partial<T, VEC, MASK>(p, j, lo, hi, x);
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int64_t e = j * VEC + c;
-      st[c].fold(e >= lo && e < hi ? load_input1<T, MASK>(p, e) : fold_identity<OP>());
+      st[c].fold(e >= lo && e < hi ? x[c] : fold_identity<OP>());
     }
   }
   int64_t j = full_lo + t;
@@ -164,10 +179,12 @@ __device__ __forceinline__ void normalize_flat(const Params& p, int g, int t, in
   const bool tail_partial = hi % VEC != 0 && tail != head;
   if ((head_partial && t == 0) || (tail_partial && t == 1)) {
     const int64_t j = t == 0 ? head : tail;
+    float x[VEC];
+    load_partial<T, VEC, MASK>(p, j, lo, hi, x);
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int64_t e = j * VEC + c;
-      if (e >= lo && e < hi) Elem<T>::put(out + e, fast_exp(load_input1<T, MASK>(p, e) - m[c]) * inv[c]);
+      if (e >= lo && e < hi) Elem<T>::put(out + e, fast_exp(x[c] - m[c]) * inv[c]);
     }
   }
   for (int64_t j = full_lo + t; j < full_hi; j += g) {

@@ -73,8 +73,7 @@ __device__ __forceinline__ void flat_vectors(const Params& p, int64_t j0, int64_
   }
   if (j1 > jv) {
     float x[VEC];
-#pragma unroll
-    for (int c = 0; c < VEC; ++c) x[c] = j1 * VEC + c < total ? load_input1<T, MASK>(p, j1 * VEC + c) : 0.f;
+    load_partial<T, VEC, MASK>(p, j1, j1 * VEC, total, x);   // components past the array are masked by body
     body(j1, x);
   }
 }

@@ -13,14 +13,14 @@ Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
   interrupted run resumes.
 * ``fit`` solves, per operation family and schedule, a nonnegative least
   squares problem on relative error (each row divided by its measured
-  time), choosing the subset of terms with the lowest leave-one-shape-out
-  error, and then the decision margin that maximises the share of training
-  cases within 3% of the faster schedule.
+  time) over all terms, reports its leave-one-shape-out error, and then
+  picks the decision margin that maximises the share of training cases
+  within 3% of the faster schedule.
 * ``evaluate`` reports, for a suite's measurements, how many choices fall
   within 3% of the faster measured schedule.
 
     python -m ragged.calibrate measure --suite train --out train.jsonl
-    python -m ragged.calibrate fit train.jsonl --out cost_model.json
+    python -m ragged.calibrate fit train.jsonl --out cost_model.json [--heldout heldout.jsonl]
     python -m ragged.calibrate evaluate heldout.jsonl [--model cost_model.json]
 """
 from __future__ import annotations
@@ -36,6 +36,7 @@ import time
 
 import numpy as np
 
+from .optimizations import Optimizations
 from .selection import FAMILIES, SCHEDULES, TERMS, VERSION, CostModel, family, features
 from .workloads import make_lengths, offsets_from_lengths
 
@@ -147,7 +148,7 @@ def measure(cases: list[Case], out: Path, *, log=print) -> int:
                 run()
                 times[schedule] = round(_time_calls(torch, run), 2)
             record = {**asdict(case), "key": case.key, "max_len": max_len, "fused": bool(program.metadata["fused"]),
-                      "us": times}
+                      "mapping": program.metadata["mapping"], "us": times}
             sink.write(json.dumps(record) + "\n")
             sink.flush()
             measured += 1
@@ -167,9 +168,15 @@ def _family(record: dict) -> str:
     return family(record["op"], bool(record.get("fused", False)))
 
 
+def _flat(record: dict) -> bool:
+    mapping = record.get("mapping") or Optimizations().geometry(record["d"], record["dtype"])[2]
+    return mapping == "flat"
+
+
 def _row(record: dict) -> np.ndarray:
     element = 2 if record["dtype"] == "bf16" else 4
-    return np.array(features(record["n"], record["b"], record["d"], record["max_len"], element, record["op"]))
+    return np.array(features(record["n"], record["b"], record["d"], record["max_len"], element, record["op"],
+                             flat=_flat(record)))
 
 
 def _nnls(a: np.ndarray, y: np.ndarray) -> np.ndarray:
@@ -193,27 +200,22 @@ def _shape_key(record: dict) -> tuple:
 
 
 def fit_family(records: list[dict], schedule: str) -> tuple[np.ndarray, float]:
-    """Coefficients for one family and schedule: the term subset (constant
-    always in) with the lowest leave-one-shape-out mean relative error."""
+    """Coefficients for one family and schedule over all terms, and the
+    mean relative error of the same fit when each shape is left out."""
     rows = np.array([_row(r) for r in records])
     times = np.array([r["us"][schedule] for r in records], dtype=np.float64)
     shapes = [_shape_key(r) for r in records]
-    groups = sorted(set(shapes))
-    best, best_error = None, math.inf
-    for bits in range(1 << (TERMS - 1)):
-        mask = (True,) + tuple(bool(bits >> i & 1) for i in range(TERMS - 1))
-        errors = []
-        for group in groups:
-            train = np.array([s != group for s in shapes])
-            if train.sum() < sum(mask):
-                continue
-            coef = _fit_relative(rows[train], times[train], mask)
-            test = ~train
-            errors.extend(np.abs(rows[test] @ coef - times[test]) / times[test])
-        error = float(np.mean(errors)) if errors else math.inf
-        if error < best_error:
-            best, best_error = mask, error
-    return _fit_relative(rows, times, best), best_error
+    every = (True,) * TERMS
+    errors = []
+    for group in sorted(set(shapes)):
+        train = np.array([s != group for s in shapes])
+        if train.sum() < TERMS:
+            continue
+        coef = _fit_relative(rows[train], times[train], every)
+        test = ~train
+        errors.extend(np.abs(rows[test] @ coef - times[test]) / times[test])
+    error = float(np.mean(errors)) if errors else math.inf
+    return _fit_relative(rows, times, every), error
 
 
 def choices(model: CostModel, records: list[dict]) -> list[tuple[dict, str]]:
@@ -221,7 +223,7 @@ def choices(model: CostModel, records: list[dict]) -> list[tuple[dict, str]]:
     for record in records:
         element = 2 if record["dtype"] == "bf16" else 4
         chosen, _ = model.choose(record["op"], record["n"], record["b"], record["d"], record["max_len"], element,
-                                 fused=bool(record.get("fused", False)))
+                                 fused=bool(record.get("fused", False)), flat=_flat(record))
         out.append((record, chosen))
     return out
 
@@ -270,9 +272,9 @@ def fit(records: list[dict]) -> dict:
     data["margin"] = best_margin
     data["calibration"] = {
         "status": "fitted on MI355X measurements (python -m ragged.calibrate fit)",
-        "terms": "t_us = c0 + c1*M + c2*S + c3*B/1000 + c4*M*log2(skew) + c5*X_l2 + c6*X_mall",
-        "method": "per family and schedule: NNLS on relative error, term subset by leave-one-shape-out error; "
-                  "margin maximising training choices within 3% of the faster schedule",
+        "terms": "t_us = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall",
+        "method": "per family and schedule: NNLS on relative error over all terms (leave-one-shape-out error "
+                  "reported); margin maximising training choices within 3% of the faster schedule",
         "train_cases": len(records), "leave_one_shape_out_error": errors, "train_within_3pct": best_share}
     return data
 
@@ -287,6 +289,7 @@ def main(argv=None) -> int:
     f = sub.add_parser("fit")
     f.add_argument("results", type=Path)
     f.add_argument("--out", type=Path, required=True)
+    f.add_argument("--heldout", type=Path, help="held-out measurements to evaluate the fit on (recorded only)")
     e = sub.add_parser("evaluate")
     e.add_argument("results", type=Path)
     e.add_argument("--model", type=Path)
@@ -299,6 +302,12 @@ def main(argv=None) -> int:
         return 0
     if args.command == "fit":
         data = fit(load(args.results))
+        data["calibration"]["train_file"] = args.results.name
+        if args.heldout:
+            report = evaluate(CostModel.from_dict(data), load(args.heldout))
+            data["calibration"]["heldout_file"] = args.heldout.name
+            data["calibration"]["heldout_cases"] = report["cases"]
+            data["calibration"]["heldout_within_3pct"] = report["share"]
         args.out.write_text(json.dumps(data, indent=2) + "\n")
         print(json.dumps(data["calibration"], indent=2))
         return 0

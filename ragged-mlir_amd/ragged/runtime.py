@@ -106,7 +106,8 @@ class CompiledProgram:
             element = 2 if self.spec.dtype == "bf16" else 4
             choice = self._choices[key] = default_model().choose(self.spec.op, n, b, self.spec.feature_dim, max_len,
                                                                  element, l2_mib=l2_mib,
-                                                                 fused=bool(self._metadata["fused"]))
+                                                                 fused=bool(self._metadata["fused"]),
+                                                                 flat=self._metadata["mapping"] == "flat")
         return choice
 
     def close(self) -> None:

@@ -9,17 +9,20 @@ families are the reference's {reduce, softmax} plus ``softmax_fused``: a
 softmax whose classified schedule is the register-resident worker pays a
 per-segment cost the streaming worker does not, so it gets its own fit.
 
-The terms are re-derived for MI355X (model version 3, seven terms, µs):
+The terms are re-derived for MI355X (model version 4, eight terms, µs):
 
-    t = c0 + c1*M + c2*S + c3*B/1000 + c4*M*log2(skew) + c5*X_l2 + c6*X_mall
+    t = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall
 
-M = N*D / 2^18 elements; S = L*D*element_bytes / 2^20, the MiB the one
-workgroup that owns the longest segment must stream in block-per-segment;
-skew = L*B/N; X_l2 / X_mall = MiB of the call's working set (input rows plus
-output: B rows for sum/max, N for softmax) beyond the total L2 (8 XCDs x
-4 MiB) and beyond the 256 MiB Infinity Cache. The reference's single
-"beyond the 72 MiB L2" term becomes two because MI355X has two cache levels
-of very different size in front of HBM.
+W = MiB the call moves (rows read; rows written for softmax, B result rows
+for sum/max); S = L*D*element_bytes / 2^20, the MiB the one workgroup that
+owns the longest segment must stream in block-per-segment; B/1000 the
+per-segment cost, with two refinements: F = 1 for the flat mapping (D below
+the 16-byte vector: a segment is a run of elements, and block-per-segment
+pays most per segment there) and R = row KiB (D*element_bytes / 1024);
+X_l2 / X_mall = MiB of the working set (input rows plus output rows) beyond
+the total L2 (8 XCDs x 4 MiB) and beyond the 256 MiB Infinity Cache. The
+reference's single "beyond the 72 MiB L2" term becomes two because MI355X
+has two cache levels of very different size in front of HBM.
 """
 from __future__ import annotations
 
@@ -34,8 +37,8 @@ from .errors import CacheMismatch
 MODEL_PATH = Path(__file__).with_name("cost_model.json")
 SCHEDULES = ("classified", "naive")
 FAMILIES = ("reduce", "softmax", "softmax_fused")
-TERMS = 7
-VERSION = 3
+TERMS = 8
+VERSION = 4
 
 
 def family(op: str, fused: bool = False) -> str:
@@ -45,16 +48,15 @@ def family(op: str, fused: bool = False) -> str:
 
 
 def features(n: int, b: int, d: int, max_len: int, element_bytes: int = 4, op: str = "sum",
-             l2_mib: float = 32.0, mall_mib: float = 256.0) -> tuple[float, ...]:
-    """The seven prediction terms for one call."""
-    elements = n * d / 2**18
-    skew = max_len * b / n if n else 1.0
-    rows = n * d * element_bytes / 2**20
+             l2_mib: float = 32.0, mall_mib: float = 256.0, flat: bool = False) -> tuple[float, ...]:
+    """The eight prediction terms for one call."""
+    row = d * element_bytes
+    rows = n * row / 2**20
     output_rows = n if op == "softmax" else b
-    working_set = rows + output_rows * d * element_bytes / 2**20
-    return (1.0, elements, max_len * d * element_bytes / 2**20, b / 1000.0,
-            elements * math.log2(max(1.0, skew)), max(0.0, working_set - l2_mib),
-            max(0.0, working_set - mall_mib))
+    moved = rows + output_rows * row / 2**20
+    segments = b / 1000.0
+    return (1.0, moved, max_len * row / 2**20, segments, segments if flat else 0.0, segments * row / 1024,
+            max(0.0, moved - l2_mib), max(0.0, moved - mall_mib))
 
 
 @dataclass(frozen=True)
@@ -88,20 +90,21 @@ class CostModel:
         return cls.from_dict(json.loads(Path(path).read_text()))
 
     def predict(self, schedule: str, op: str, n: int, b: int, d: int, max_len: int, element_bytes: int = 4,
-                l2_mib: float | None = None, fused: bool = False) -> float:
+                l2_mib: float | None = None, fused: bool = False, flat: bool = False) -> float:
         terms = features(n, b, d, max_len, element_bytes, op, self.l2_mib if l2_mib is None else l2_mib,
-                         self.mall_mib)
+                         self.mall_mib, flat)
         return sum(c * x for c, x in zip(self.coefficients[family(op, fused)][schedule], terms))
 
     def choose(self, op: str, n: int, b: int, d: int, max_len: int | None, element_bytes: int = 4,
-               l2_mib: float | None = None, fused: bool = False) -> tuple[str, dict[str, Any]]:
+               l2_mib: float | None = None, fused: bool = False,
+               flat: bool = False) -> tuple[str, dict[str, Any]]:
         """The schedule to run and the inputs and predictions behind it."""
         if max_len is None:
             return "classified", {"max_len": None, "reason": "no length statistics on the host"}
         if l2_mib is not None and not (isinstance(l2_mib, (int, float)) and l2_mib > 0):
             raise ValueError("l2_mib must be a positive capacity in MiB")
-        classified = self.predict("classified", op, n, b, d, max_len, element_bytes, l2_mib, fused)
-        naive = self.predict("naive", op, n, b, d, max_len, element_bytes, l2_mib, fused)
+        classified = self.predict("classified", op, n, b, d, max_len, element_bytes, l2_mib, fused, flat)
+        naive = self.predict("naive", op, n, b, d, max_len, element_bytes, l2_mib, fused, flat)
         selected = "classified" if classified < naive * (1 - self.margin) else "naive"
         return selected, {"max_len": max_len, "l2_mib": self.l2_mib if l2_mib is None else l2_mib,
                           "predicted_us": {"classified": round(classified, 2), "naive": round(naive, 2)}}

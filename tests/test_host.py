@@ -154,13 +154,15 @@ def test_status_decoding_known_answers():
 
 
 def test_cost_model_features_known_answer():
-    # N = 2^20 rows, B = 1024, D = 4 f32, L = 2^14: M = 16, S = 2^14*4*4/2^20 = 0.25 MiB,
-    # skew = 2^14*1024/2^20 = 16 -> M*log2(skew) = 64; working set (N + B rows) = 16.015625 MiB,
-    # under the 32 MiB L2.
-    assert features(2**20, 1024, 4, 2**14, 4, "sum") == (1.0, 16.0, 0.25, 1.024, 64.0, 0.0, 0.0)
-    # Softmax writes N rows: 128 MiB of rows at D=32 f32 -> 256 MiB working set.
+    # N = 2^20 rows, B = 1024, D = 4 f32 (16-byte rows), L = 2^14: W = 16 MiB of rows read + 1024
+    # result rows = 16.015625 MiB; S = 2^14*16/2^20 = 0.25 MiB; B/1000 = 1.024; row mapping (F = 0);
+    # R*B/1000 = 1.024 * 16/1024; the working set is under the 32 MiB L2.
+    assert features(2**20, 1024, 4, 2**14, 4, "sum") == (1.0, 16.015625, 0.25, 1.024, 0.0, 1.024 * 16 / 1024,
+                                                          0.0, 0.0)
+    assert features(2**20, 1024, 4, 2**14, 4, "sum", flat=True)[4] == 1.024
+    # Softmax writes N rows: 128 MiB of rows at D=32 f32 -> 256 MiB moved.
     f = features(2**20, 1024, 32, 2**14, 4, "softmax")
-    assert f[5] == pytest.approx(256.0 - 32.0) and f[6] == 0.0
+    assert f[1] == 256.0 and f[6] == pytest.approx(256.0 - 32.0) and f[7] == 0.0
 
 
 def test_product_fails_loudly_without_the_library(monkeypatch, tmp_path):
