@@ -20,8 +20,12 @@ Pinning (what fails if the restatement is wrong):
 * ``quantize_bf16``: the reference's RNE known answers (test_oracle.py:111-118)
   and an exhaustive check against torch's own bfloat16 rounding.
 * ``masked_logits``: closed-form f32 arithmetic checks (tests/test_oracle.py).
+* ``offsets_errors``: the reference's all-conditions known answer
+  (test/gpu/test_checked.py:125-130) and brute-force properties
+  (tests/test_oracle.py).
 """
 
+from .offsets import CONDITIONS, offsets_errors
 from .reference import (
     STRICT_TOLERANCES,
     TOLERANCES,
@@ -42,5 +46,5 @@ __all__ = [
     "STRICT_TOLERANCES",
     "TOLERANCES", "assert_matches", "quantize_bf16", "segment_max", "segment_max_loop",
     "segment_reduce", "segment_softmax", "segment_softmax_loop", "segment_sum", "segment_sum_loop",
-    "validate_offsets", "masked_logits", "assert_masked_softmax_matches",
+    "validate_offsets", "masked_logits", "assert_masked_softmax_matches", "CONDITIONS", "offsets_errors",
 ]

@@ -326,3 +326,61 @@ def test_strict_tolerance_table_is_tighter_and_rejects_what_it_should():
     with pytest.raises(AssertionError):
         oracle.assert_matches(off, values, offsets, operation="sum", input_dtype="f32",
                               tolerances=oracle.STRICT_TOLERANCES)
+
+
+# ---------------------------------------------------------------------------
+# Checked-mode offsets conditions (oracle/offsets.py).
+
+def test_offsets_errors_known_answer():
+    """The reference's all-conditions case (test/gpu/test_checked.py:125-130):
+    N = 8, min_len = max_len = 4."""
+    from oracle import CONDITIONS, offsets_errors
+    errors = offsets_errors([1, -2, -3, 11, 10, 0, 1, 7, 6], 8, 4, 4)
+    assert errors == dict(zip(CONDITIONS, [0, 8, 1, 3, 0, 5, 6]))
+    assert list(errors) == list(CONDITIONS)         # slot order
+
+
+def test_offsets_errors_single_conditions():
+    from oracle import offsets_errors
+    assert offsets_errors([0, 4, 8], 8) == {}
+    assert offsets_errors([1, 4, 8], 8) == {"first_nonzero": 0}
+    assert offsets_errors([0, 4, 7], 8) == {"final_mismatch": 2}
+    assert offsets_errors([0, -1, 8], 8) == {"negative": 1, "nonmonotone": 0}
+    assert offsets_errors([0, 9, 8], 8) == {"above_n": 1, "nonmonotone": 1}
+    assert offsets_errors([0, 4, 3, 8], 8) == {"nonmonotone": 1}
+    # B = 0: the only offset is both the first and the final one.
+    assert offsets_errors([1], 0) == {"first_nonzero": 0, "final_mismatch": 0, "above_n": 0}
+    assert offsets_errors([0], 2) == {"final_mismatch": 0}
+    # Hints apply only to in-range monotone segments; the extreme pair is
+    # never subtracted (it would overflow in i64).
+    lo, hi = -(1 << 63), (1 << 63) - 1
+    assert offsets_errors([0, lo, hi, 0, 8], 8, 9, 8) == {
+        "negative": 1, "above_n": 2, "nonmonotone": 0, "below_min_len": 3}
+
+
+def test_offsets_errors_brute_force():
+    """Against an independent formulation on random small offsets: scan the
+    pairs and offsets in index order and keep the first hit per condition."""
+    from oracle import offsets_errors
+    rng = np.random.default_rng(5)
+    for _ in range(3000):
+        b = int(rng.integers(0, 6))
+        n = int(rng.integers(0, 9))
+        offsets = [int(v) for v in rng.integers(-3, 12, size=b + 1)]
+        min_len = None if rng.random() < 0.3 else int(rng.integers(0, 5))
+        max_len = None if rng.random() < 0.3 else int(rng.integers(0, 6))
+        expected = {}
+        checks = [("first_nonzero", [0] if offsets[0] != 0 else []),
+                  ("final_mismatch", [b] if offsets[-1] != n else []),
+                  ("negative", [i for i in range(b + 1) if offsets[i] < 0]),
+                  ("above_n", [i for i in range(b + 1) if offsets[i] > n]),
+                  ("nonmonotone", [i for i in range(b) if offsets[i + 1] < offsets[i]])]
+        valid = [i for i in range(b) if 0 <= offsets[i] <= offsets[i + 1] <= n]
+        checks.append(("below_min_len", [i for i in valid if min_len is not None
+                                         and offsets[i + 1] - offsets[i] < min_len]))
+        checks.append(("above_max_len", [i for i in valid if max_len is not None
+                                         and offsets[i + 1] - offsets[i] > max_len]))
+        for name, hits in checks:
+            if hits:
+                expected[name] = hits[0]
+        assert offsets_errors(offsets, n, min_len, max_len) == expected
