@@ -207,14 +207,17 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
 
             def timed_calls() -> float:
                 if args.cold:
-                    total_ms = 0.0
+                    total_ms, host = 0.0, []
                     for _ in range(args.steps):
                         flush.fill_(1)
                         start.record()
+                        t_host = time.perf_counter()
                         program.run(x, off, out, select=select, max_len=max_len)
+                        host.append((time.perf_counter() - t_host) * 1e6)
                         end.record()
                         torch.cuda.synchronize()
                         total_ms += start.elapsed_time(end)
+                    host_us.append([round(float(np.median(host)), 1), round(float(np.max(host)), 1)])
                     return total_ms / args.steps
                 torch.cuda.synchronize()
                 host = []
