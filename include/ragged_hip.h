@@ -59,7 +59,8 @@ enum rg_role {
   RG_ROLE_SPLIT_NORMALIZE = 6, /* softmax: normalise each part */
   RG_ROLE_NAIVE = 7,           /* block-per-segment schedule */
   RG_ROLE_FUSED = 8,           /* softmax: register-resident worker over all block/split items */
-  RG_ROLE_DEFERRED = 9,        /* softmax: re-read pass for chunks that stopped waiting */
+  RG_ROLE_DEFERRED = 9,        /* softmax: re-read pass for chunks that stopped waiting, then the
+                                  register-resident softmax's wave class */
   RG_ROLE_WORKER = 10,         /* persistent worker over the wave, block and split queues */
   RG_ROLE_COUNT = 11
 };
