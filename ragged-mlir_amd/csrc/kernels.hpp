@@ -196,12 +196,31 @@ __device__ __forceinline__ void normalize_flat(const Params& p, int g, int t, in
   }
 }
 
-// In FLAT mode component c holds feature c % D: fold components D.. into 0..D-1.
+// In FLAT mode component c holds feature c % D (D a power of two dividing
+// VEC): fold components D.. into 0..D-1, each target in increasing c. The
+// target is selected among the constant indices t < c, so no register
+// array is indexed by a run-time value (which would place it in scratch).
 template <int OP, int VEC>
 __device__ __forceinline__ void merge_components(State<OP> (&st)[VEC], int d) {
 #pragma unroll
   for (int c = 1; c < VEC; ++c) {
-    if (c >= d) st[c % d].merge(st[c]);
+#pragma unroll
+    for (int t = 0; t < c; ++t) {
+      if (c >= d && (c & (d - 1)) == t) st[t].merge(st[c]);
+    }
+  }
+}
+
+// x[c] = x[c % D] for every component (D a power of two dividing VEC), with
+// constant register indices only.
+template <int VEC>
+__device__ __forceinline__ void spread_components(float (&x)[VEC], int d) {
+#pragma unroll
+  for (int c = 1; c < VEC; ++c) {
+#pragma unroll
+    for (int t = 0; t < c; ++t) {
+      if (c >= d && (c & (d - 1)) == t) x[c] = x[t];
+    }
   }
 }
 
@@ -306,14 +325,17 @@ __device__ __forceinline__ void process_segment(const Params& p, int64_t s, int6
       float m[VEC], inv[VEC];
       softmax_factors<VEC>(st, m, inv);
       // Component c of every vector belongs to feature c % D.
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) { m[c] = m[c % p.d]; inv[c] = inv[c % p.d]; }
+      spread_components<VEC>(m, p.d);
+      spread_components<VEC>(inv, p.d);
       normalize_flat<T, VEC, MASK>(p, G, t, lo, hi, m, inv);
     } else if (t == 0) {
       float x[VEC];
       result_of<OP, VEC>(st, x);
       T* out = static_cast<T*>(p.out) + s * p.d;
-      for (int f = 0; f < p.d; ++f) Elem<T>::put(out + f, x[f]);
+#pragma unroll
+      for (int f = 0; f < VEC; ++f) {
+        if (f < p.d) Elem<T>::put(out + f, x[f]);
+      }
     }
   } else {
     const RowGeo g = row_geo<VEC>(p.d, G, t, tile);

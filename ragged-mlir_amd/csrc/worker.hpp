@@ -118,14 +118,83 @@ __device__ __forceinline__ void fold_residues(float (&x)[VEC], int d) {
   }
 }
 
+// Vectors a lane holds in registers for a short flat segment (48 floats).
+template <int VEC>
+constexpr int kLaneVectors = 48 / VEC;
+
+// Softmax of a flat-mapped segment of at most kLaneVectors whole vectors by
+// one lane, held in registers: all loads in one round, then column max,
+// exp(x - ref) in place, column sums and the stores. A column of only -inf
+// has no mass (ref 0). Vectors past j1 re-read vector j1 and are not used.
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void lane_softmax_held(const Params& p, int64_t lo, int64_t hi, int64_t j0, int64_t j1) {
+  constexpr int K = kLaneVectors<VEC>;
+  const int d = p.d;
+  float x[K][VEC];
+#pragma unroll
+  for (int u = 0; u < K; ++u) load_input<T, VEC, MASK>(p, (j0 + u <= j1 ? j0 + u : j1) * VEC, x[u]);
+  auto inside = [&](int u, int c) {
+    const int64_t e = (j0 + u) * VEC + c;
+    return j0 + u <= j1 && e >= lo && e < hi;
+  };
+  float m[VEC], ref[VEC], s[VEC], inv[VEC];
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) m[c] = neg_inf();
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) m[c] = inside(u, c) ? fmax_nan(m[c], x[u][c]) : m[c];
+  }
+  fold_residues<true, VEC>(m, d);
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) {
+    ref[c] = m[c] == neg_inf() ? 0.f : m[c];
+    s[c] = 0.f;
+  }
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      x[u][c] = fast_exp(x[u][c] - ref[c]);
+      s[c] += inside(u, c) ? x[u][c] : 0.f;
+    }
+  }
+  fold_residues<false, VEC>(s, d);
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) inv[c] = fast_exp(m[c] - m[c]) / s[c];   // 1 / s, or NaN for an all -inf column
+  T* out = static_cast<T*>(p.out);
+#pragma unroll
+  for (int u = 0; u < K; ++u) {
+    if (j0 + u > j1) break;
+    const int64_t j = j0 + u;
+    float y[VEC];
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) y[c] = x[u][c] * inv[c];
+    if (j * VEC >= lo && j * VEC + VEC <= hi) {
+      Elem<T>::template store<VEC>(out + j * VEC, y);   // a whole vector of this segment
+    } else {
+#pragma unroll
+      for (int c = 0; c < VEC; ++c) {
+        if (inside(u, c)) Elem<T>::put(out + j * VEC + c, y[c]);
+      }
+    }
+  }
+}
+
 // Softmax of a flat-mapped segment by one lane: column max, column sum of
-// exp(x - ref) and the normalised values, three passes over its elements
-// (re-read from cache). A column of only -inf has no mass (ref 0).
+// exp(x - ref) and the normalised values. A segment of at most kLaneVectors
+// whole vectors is held in registers (one read); a longer one, or the one
+// that reaches the array's partial last vector, takes three passes over
+// its elements (re-read from cache). A column of only -inf has no mass.
 template <class T, int VEC, bool MASK>
 __device__ __forceinline__ void lane_softmax(const Params& p, int64_t lo, int64_t hi) {
   if (lo >= hi) return;
   const int d = p.d;
   const int64_t j0 = lo / VEC, j1 = (hi - 1) / VEC;
+  if (j1 - j0 < kLaneVectors<VEC> && j1 < p.n * p.d / VEC) {
+    lane_softmax_held<T, VEC, MASK>(p, lo, hi, j0, j1);
+    return;
+  }
   // Every pass visits the segment's vectors four at a time (four loads in
   // flight per lane).
   auto pass = [&](auto&& body) { flat_vectors<4, T, VEC, MASK>(p, j0, j1, body); };
@@ -185,7 +254,10 @@ __device__ __forceinline__ void lane_segment(const Params& p, int64_t s, int64_t
     lane_fold<OP, T, VEC, MASK>(p, lo, hi, st);
     merge_components<OP, VEC>(st, p.d);
     T* out = static_cast<T*>(p.out) + s * p.d;
-    for (int f = 0; f < p.d; ++f) Elem<T>::put(out + f, value_of<OP>(st[f]));
+#pragma unroll
+    for (int f = 0; f < VEC; ++f) {
+      if (f < p.d) Elem<T>::put(out + f, value_of<OP>(st[f]));
+    }
   }
   if (p.visits) atomicAdd(p.visits + s, 1);
 }
@@ -270,9 +342,12 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
     merge_components<OP, VEC>(st, p.d);
     block_reduce<OP, VEC>(st, 1, 0, lds);
     if (t == 0) {
-      for (int f = 0; f < p.d; ++f) {
-        publish(p.partials + item * p.d + f, value_of<OP>(st[f]));
-        if constexpr (OP == OP_SOFTMAX) publish(p.partial_sums + item * p.d + f, st[f].s);
+#pragma unroll
+      for (int f = 0; f < VEC; ++f) {
+        if (f < p.d) {
+          publish(p.partials + item * p.d + f, value_of<OP>(st[f]));
+          if constexpr (OP == OP_SOFTMAX) publish(p.partial_sums + item * p.d + f, st[f].s);
+        }
       }
     }
   } else {
