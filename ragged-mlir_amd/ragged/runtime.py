@@ -83,6 +83,7 @@ class CompiledProgram:
         # so they can share it; it grows to the largest plan seen.
         self._workspaces: dict[tuple[int, int], Any] = {}
         self._names = {kernel["role"]: kernel["name"] for kernel in self._metadata["kernels"]}
+        self._alone: int | None = None
 
     @property
     def selects(self) -> bool:
@@ -205,15 +206,24 @@ class CompiledProgram:
             if module is None:
                 if self.artifact.key.library_sha256 != native.library_sha256():
                     raise CacheMismatch("artifact was built for a different libragged_hip.so; recompile")
-                metadata = self._metadata
-                thresholds = metadata["thresholds"] or [-1, -1]
-                spec = native.make_spec(self.spec.op, self.spec.dtype, self.spec.offsets_dtype, self.spec.feature_dim,
-                                        scale=self.spec.scale, mask=self.spec.mask,
-                                        vectorize=self.spec.optimizations.vectorize,
-                                        debug_visits=self.spec.debug_visits, t_wave=thresholds[0],
-                                        t_block=thresholds[1], part_rows=metadata["part_rows"] or -1)
-                module = _modules[key] = native.NativeModule(device, spec)
+                module = _modules[key] = native.NativeModule(device, self._native_spec())
             return module
+
+    def _native_spec(self) -> native.Spec:
+        """The library's specialisation of this program (thresholds from the
+        manifest, defaults filled by the library)."""
+        metadata = self._metadata
+        thresholds = metadata["thresholds"] or [-1, -1]
+        return native.make_spec(self.spec.op, self.spec.dtype, self.spec.offsets_dtype, self.spec.feature_dim,
+                                scale=self.spec.scale, mask=self.spec.mask,
+                                vectorize=self.spec.optimizations.vectorize, debug_visits=self.spec.debug_visits,
+                                t_wave=thresholds[0], t_block=thresholds[1], part_rows=metadata["part_rows"] or -1)
+
+    def _alone_rows(self) -> int:
+        """Longest segment one lane or lane group reduces alone (0: none)."""
+        if self._alone is None:
+            self._alone = int(self._native_spec().alone_rows)
+        return self._alone
 
     def _plan(self, module: native.NativeModule, n: int, b: int, schedule: str) -> native.Plan:
         key = (module.device, n, b, schedule)
@@ -245,6 +255,10 @@ class CompiledProgram:
         if self.naive is not None and select != "classified":
             if select == "naive":
                 chosen, selection = "naive", {"forced": True}
+            elif self._short_segments(max_len):
+                # One worker launch reduces every segment alone: cheaper than
+                # both modelled schedules, so the model is not consulted.
+                chosen, selection = "classified", {"max_len": max_len, "reason": "every segment reduced alone"}
             else:
                 try:
                     n, b = int(values.shape[0]), int(offsets.numel()) - 1
@@ -271,7 +285,7 @@ class CompiledProgram:
             optimizations=metadata["optimizations"], d_tile=metadata["d_tile"], d_vector=metadata["d_vector"],
             resources=None, streams=1, selected=selected, selection=selection)
 
-    def _short_segments(self, module: native.NativeModule, max_len: int | None) -> bool:
+    def _short_segments(self, max_len: int | None) -> bool:
         """Whether the caller's max_len lets one lane (or lane group) reduce
         every segment alone: then one worker launch takes the segments in
         order (no classify, no workspace). A max_len that is too small only
@@ -279,7 +293,7 @@ class CompiledProgram:
         thresholds = self._metadata["thresholds"]
         return (self._schedule == "classified" and max_len is not None
                 and not self.spec.debug_visits and bool(thresholds) and 0 < thresholds[0]
-                and 0 < module.spec.alone_rows and max_len <= module.spec.alone_rows)
+                and 0 < self._alone_rows() and max_len <= self._alone_rows())
 
     def _run(self, values, offsets, out, stream, mode, *, debug_buffers, mask, selected, selection,
              max_len: int | None = None) -> ExecutionReport:
@@ -328,7 +342,7 @@ class CompiledProgram:
                 if b == 0:
                     return self._report(started, names, grids, 0, mode=mode, selected=selected, selection=selection,
                                         validation_bytes=validation_bytes, validation_ms=validation_ms)
-            short = self._short_segments(module, max_len)
+            short = self._short_segments(max_len)
             if short:
                 selection = {**selection, "short_segments": True}
             plan = self._plan(module, n, b, "short" if short else self._schedule)
