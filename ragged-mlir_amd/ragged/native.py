@@ -9,7 +9,6 @@ This replaces the reference's nanobind module ``ragged._native``
 from __future__ import annotations
 
 import ctypes
-from functools import lru_cache
 import hashlib
 from pathlib import Path
 import threading
@@ -101,9 +100,15 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
     return lib
 
 
-@lru_cache(maxsize=1)
+_loaded: dict[Path, ctypes.CDLL] = {}   # LIBRARY_PATH -> declared library
+
+
 def library() -> ctypes.CDLL:
-    """The in-tree HIP library; RuntimeUnavailable if it was not built."""
+    """The in-tree HIP library, loaded and declared once per path;
+    RuntimeUnavailable if it was not built."""
+    lib = _loaded.get(LIBRARY_PATH)
+    if lib is not None:
+        return lib
     if not LIBRARY_PATH.is_file():
         raise RuntimeUnavailable(f"native HIP library is missing: {LIBRARY_PATH}; run "
                                  "`python ragged-mlir_amd/build.py` (no CPU execution fallback exists)")
@@ -112,9 +117,16 @@ def library() -> ctypes.CDLL:
             lib = _declare(ctypes.CDLL(str(LIBRARY_PATH)))
         except OSError as exc:
             raise RuntimeUnavailable(f"cannot load {LIBRARY_PATH}: {exc}") from exc
-    if lib.rg_abi_version() != ABI_VERSION:
-        raise RuntimeUnavailable(f"{LIBRARY_PATH.name} ABI {lib.rg_abi_version()} != {ABI_VERSION}")
+        if lib.rg_abi_version() != ABI_VERSION:
+            raise RuntimeUnavailable(f"{LIBRARY_PATH.name} ABI {lib.rg_abi_version()} != {ABI_VERSION}")
+        _loaded[LIBRARY_PATH] = lib
     return lib
+
+
+def plan_ref(plan: "Plan"):
+    """The by-reference argument ``rg_run`` takes for ``plan`` (keep ``plan``
+    alive while it is used)."""
+    return ctypes.byref(plan)
 
 
 def library_sha256() -> str:
@@ -169,7 +181,8 @@ class NativeModule:
         self.device = device
         self.spec = spec
         handle = ctypes.c_void_p()
-        _check(library().rg_module_create(device, ctypes.byref(spec), ctypes.byref(handle)), "rg_module_create")
+        self._lib = library()
+        _check(self._lib.rg_module_create(device, ctypes.byref(spec), ctypes.byref(handle)), "rg_module_create")
         self._handle = handle
 
     def resident_blocks(self, role: str) -> int:
@@ -186,8 +199,15 @@ class NativeModule:
 
     def run(self, plan: Plan, values: int, offsets: int, out: int, mask: int | None, workspace: int | None,
             workspace_bytes: int, stream: int) -> None:
-        _check(library().rg_run(self._handle, ctypes.byref(plan), values, offsets, out, mask, workspace,
-                                workspace_bytes, stream), "rg_run")
+        self.run_ref(plan_ref(plan), values, offsets, out, mask, workspace, workspace_bytes, stream)
+
+    def run_ref(self, plan, values: int, offsets: int, out: int, mask: int | None, workspace: int | None,
+                workspace_bytes: int, stream: int) -> None:
+        """``run`` with ``plan`` already a ctypes reference (``plan_ref``)."""
+        status = self._lib.rg_run(self._handle, plan, values, offsets, out, mask, workspace, workspace_bytes,
+                                  stream)
+        if status:
+            _check(status, "rg_run")
 
     def set_spin_limit(self, microseconds: int) -> None:
         """Bound of a softmax chunk's wait for its segment (test control)."""

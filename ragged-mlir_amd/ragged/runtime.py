@@ -13,6 +13,7 @@ missing library or a non-gfx950 device raise ``RuntimeUnavailable``.
 """
 from __future__ import annotations
 
+import contextlib
 import importlib
 import json
 import threading
@@ -29,15 +30,23 @@ from .validation import raise_for_status, validate_program
 _lock = threading.RLock()
 _modules: dict[tuple[int, str], native.NativeModule] = {}   # (device, artifact digest) -> module
 _device_arch: dict[int, str] = {}
+_device_runs: dict[tuple[int, str], bool] = {}     # (device, chip) -> the chip's code runs there
 _device_l2_mib: dict[int, float | None] = {}
 I64_MAX = 2**63 - 1
 
 
+_torch_module = None
+
+
 def _torch():
-    try:
-        return importlib.import_module("torch")
-    except ImportError as exc:
-        raise RuntimeUnavailable("PyTorch is not installed; install PyTorch-ROCm to execute") from exc
+    """torch, imported on first use (``import ragged`` never imports it)."""
+    global _torch_module
+    if _torch_module is None:
+        try:
+            _torch_module = importlib.import_module("torch")
+        except ImportError as exc:
+            raise RuntimeUnavailable("PyTorch is not installed; install PyTorch-ROCm to execute") from exc
+    return _torch_module
 
 
 def device_l2_mib(values) -> float | None:
@@ -79,6 +88,9 @@ class CompiledProgram:
         self.naive = naive
         self._choices: dict[tuple, tuple[str, dict[str, Any]]] = {}
         self._plans: dict[tuple[int, int, int, str], native.Plan] = {}
+        # Per plan: its kernel names and grids for reports, and the ctypes
+        # reference rg_run takes (built once, not per call).
+        self._launches: dict[tuple[int, int, int, str], tuple[list, list, Any]] = {}
         # Workspace per (device, stream): calls on one stream run in order,
         # so they can share it; it grows to the largest plan seen.
         self._workspaces: dict[tuple[int, int], Any] = {}
@@ -226,13 +238,23 @@ class CompiledProgram:
         return self._alone
 
     def _plan(self, module: native.NativeModule, n: int, b: int, schedule: str) -> native.Plan:
+        return self._plan_launches(module, n, b, schedule)[0]
+
+    def _plan_launches(self, module: native.NativeModule, n: int, b: int, schedule: str):
+        """(plan, kernel names, grids, ctypes reference) for (N, B, schedule)."""
         key = (module.device, n, b, schedule)
         plan = self._plans.get(key)
         if plan is None:
             if len(self._plans) >= 256:
                 self._plans.clear()
+                self._launches.clear()
             plan = self._plans[key] = module.plan(n, b, schedule)
-        return plan
+        launches = self._launches.get(key)
+        if launches is None:
+            steps = plan.steps
+            launches = self._launches[key] = ([self._kernel_name(role) for role, _, _, _ in steps],
+                                              [grid for _, grid, _, _ in steps], native.plan_ref(plan))
+        return (plan,) + launches
 
     # ------------------------------------------------------------------
     def run(self, values, offsets, out, stream=None, mode: str = "validated", *,
@@ -311,10 +333,15 @@ class CompiledProgram:
         if b == 0 and not checked:
             return self._report(started, mode=mode, selected=selected, selection=selection)
         device = values.device.index if values.device.index is not None else torch.cuda.current_device()
-        with torch.cuda.device(device):
-            if device not in _device_arch:
-                _device_arch[device] = torch.cuda.get_device_properties(device).gcnArchName
-            if not runs_on(self.spec.chip, _device_arch[device]):
+        # Switch devices only when the tensors are not on the current one.
+        switch = device != torch.cuda.current_device()
+        with torch.cuda.device(device) if switch else contextlib.nullcontext():
+            runs = _device_runs.get((device, self.spec.chip))
+            if runs is None:
+                if device not in _device_arch:
+                    _device_arch[device] = torch.cuda.get_device_properties(device).gcnArchName
+                runs = _device_runs[(device, self.spec.chip)] = runs_on(self.spec.chip, _device_arch[device])
+            if not runs:
                 raise RuntimeUnavailable(f"compiled target {self.spec.chip} does not run on the current device "
                                          f"({_device_arch[device]})")
             active = stream if stream is not None else torch.cuda.current_stream(device)
@@ -345,7 +372,8 @@ class CompiledProgram:
             short = self._short_segments(max_len)
             if short:
                 selection = {**selection, "short_segments": True}
-            plan = self._plan(module, n, b, "short" if short else self._schedule)
+            plan, plan_names, plan_grids, plan_ref = self._plan_launches(module, n, b,
+                                                                         "short" if short else self._schedule)
             workspace = None
             if plan.workspace_bytes:
                 workspace = self._workspace(torch, values.device, active, int(plan.workspace_bytes),
@@ -353,13 +381,12 @@ class CompiledProgram:
             inputs = [values, offsets, out] + ([mask] if mask is not None else [])
             for tensor in inputs:
                 tensor.record_stream(active)
-            module.run(plan, values.data_ptr(), offsets.data_ptr(), out.data_ptr(),
-                       mask.data_ptr() if mask is not None else None,
-                       workspace.data_ptr() if workspace is not None else None, int(plan.workspace_bytes),
-                       active.cuda_stream)
-            for role, grid, _, _ in plan.steps:
-                names.append(self._kernel_name(role))
-                grids.append(grid)
+            module.run_ref(plan_ref, values.data_ptr(), offsets.data_ptr(), out.data_ptr(),
+                           mask.data_ptr() if mask is not None else None,
+                           workspace.data_ptr() if workspace is not None else None, int(plan.workspace_bytes),
+                           active.cuda_stream)
+            names += plan_names
+            grids += plan_grids
             if debug_buffers is not None and workspace is not None:
                 dtypes = {"class_counts": torch.int64, "segment_ids": torch.int64, "item_segments": torch.int64,
                           "part_begin": torch.int64, "partials": torch.float32, "partial_sums": torch.float32,
