@@ -3,7 +3,8 @@
 //
 // Items (descriptors written by k_classify): every chunk of every
 // split-class segment (ceil(L / part_rows) chunks, contiguous in the queue),
-// then every block- and wave-class segment. A 256-thread workgroup takes the next item
+// then every block-class segment (wave-class segments are batched by
+// k_softmax_deferred after this kernel). A 256-thread workgroup takes the next item
 // with one atomic ticket (and prefetches the following descriptor while it
 // finishes) and holds its rows in registers (RPT rows per thread):
 //   1. m = column max of the rows (IEEE maximum: NaN propagates);

@@ -5,18 +5,21 @@
 // (reference ToGPU.cpp:901-998, wave64 thresholds). The reference then runs
 // one persistent kernel chain per class on forked streams
 // (ToGPU.cpp:999-1045, Driver.cpp:299-353). Here one persistent launch
-// drains all three by atomic ticket, longest work first:
+// drains all of them by atomic ticket (16 interleaved ticket counters: one
+// address serialises atomics), longest work first:
 //   1. the parts of split segments; the part that arrives last at its
 //      segment's counter folds every part in part order (deterministic) and
 //      writes the result (sum, max) or the merged statistics (softmax, then
 //      normalised by k_split_normalize) -- the reference's split_combine
 //      (ToGPU.cpp:399-472) without a separate launch;
 //   2. block-class segments, one workgroup each;
-//   3. wave-class segments, 64 per wave. A segment of at most kLaneElems
-//      elements in the flat mapping (D below the vector width) is reduced by
-//      one lane on its own -- a batch of short segments costs one pass of
-//      64 lanes instead of 64 wave-wide reductions; longer ones are reduced
-//      by the whole wave, one after the other.
+//   3. wave-class segments longer than alone_rows, one wave each (queued
+//      from the back of the wave queue);
+//   4. batches of wave-class segments of at most alone_rows rows, each
+//      reduced alone by one lane (flat mapping, D below the vector width) or
+//      by the group of lanes that holds a row -- a batch costs one pass of
+//      the wave instead of one wave-wide reduction per segment.
+// The short-segment schedule runs only step 4, over every segment in order.
 #pragma once
 
 #include "kernels.hpp"

@@ -123,6 +123,13 @@ def library() -> ctypes.CDLL:
     return lib
 
 
+def forget_library() -> None:
+    """Drop the declared library of LIBRARY_PATH (after a rebuild, so the
+    next ``library()`` opens and checks it again)."""
+    with _lock:
+        _loaded.pop(LIBRARY_PATH, None)
+
+
 def plan_ref(plan: "Plan"):
     """The by-reference argument ``rg_run`` takes for ``plan`` (keep ``plan``
     alive while it is used)."""
