@@ -277,7 +277,8 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
     if (err != hipSuccess) break;
     module->lds[role] = (uint32_t)attributes.sharedSizeBytes;
     int per_cu = 0;
-    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, module->roles[role], rg::kBlock, 0);
+    const int threads = role == RG_ROLE_CLASSIFY ? rg::kClassifyBlock : rg::kBlock;
+    err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, module->roles[role], threads, 0);
     if (err != hipSuccess) break;
     module->resident[role] = (int64_t)std::max(per_cu, 1) * prop.multiProcessorCount;
   }
@@ -400,13 +401,13 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   plan->flat = geo.flat ? 1 : 0;
   if (b == 0) return RG_OK;
 
-  auto add_launch = [&](int role, int64_t gx, int64_t gy) {
+  auto add_launch = [&](int role, int64_t gx, int64_t gy, int block = rg::kBlock) {
     const int i = plan->launches++;
     plan->roles[i] = role;
     plan->grid[i][0] = (uint32_t)std::min<int64_t>(std::max<int64_t>(gx, 1), kGridMax);
     plan->grid[i][1] = (uint32_t)std::max<int64_t>(gy, 1);
     plan->grid[i][2] = 1;
-    plan->block[i] = rg::kBlock;
+    plan->block[i] = (uint32_t)block;
     plan->lds_bytes[i] = module->lds[role];
   };
   const int64_t tiles_block = feature_tiles(d, geo.vec, geo.flat, rg::kBlock);
@@ -477,7 +478,8 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   // register-resident softmax (8 slots per thread), one for a plain reset.
   const int64_t init_work = module->fused ? items_cap * d : 0;
   add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, init_work / (rg::kBlock * 8))), 1);
-  add_launch(RG_ROLE_CLASSIFY, (b + rg::kBlock - 1) / rg::kBlock, 1);
+  const int classify_block = b >= rg::kClassifyLarge ? rg::kClassifyBlock : rg::kBlock;
+  add_launch(RG_ROLE_CLASSIFY, (b + classify_block - 1) / classify_block, 1, classify_block);
   if (module->fused) {
     // The block and split classes held in registers; then the deferred
     // chunks and the wave class, in the streaming worker's batches.

@@ -43,6 +43,13 @@ constexpr int kGroupRows = 32;         // classified worker: rows one lane group
 // atomics on one address serialise at about 12.5 ns each on MI355X, on 16
 // addresses at about 1 ns per ticket.
 constexpr int kTicketLanes = 16;
+// k_classify reserves queue runs with one atomic per class per workgroup,
+// and those atomics serialise: from kClassifyLarge segments on it runs
+// kClassifyBlock-thread workgroups (fewer atomics), below that kBlock ones
+// (more workgroups for the per-segment descriptor writes).
+constexpr int kClassifyBlock = 1024;
+constexpr int kClassifyWaves = kClassifyBlock / kWave;
+constexpr int64_t kClassifyLarge = 16384;
 constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits

@@ -464,8 +464,9 @@ __global__ __launch_bounds__(kBlock) void k_init(Params p) {
 // wave's run of queue positions, so a wave's segments of one class sit in
 // consecutive positions in segment order (classified-abi.md:56-66).
 template <class OffT>
-__global__ __launch_bounds__(kBlock) void k_classify(Params p) {
-  const int64_t s = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+__global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
+  const int64_t s = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int waves = (int)(blockDim.x / kWave);   // kWavesPerBlock or kClassifyWaves
   const int lane = threadIdx.x & (kWave - 1);
   const bool active = s < p.b;
   int64_t length = 0, start = 0;
@@ -479,13 +480,14 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
   // (back of the wave queue); runs 1, 2: block and split classes.
   const int cls = length <= p.t_wave ? (length <= p.alone_rows ? 0 : 3) : (length <= p.t_block ? 1 : 2);
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-  // Queue runs: the workgroup reserves each class's run with one atomic
-  // (not one per wave: every wave of the grid adding to the same three
-  // counters serialises at the memory side), and each wave takes its part
+  // Queue runs: the workgroup (kBlock threads, or kClassifyBlock for many
+  // segments) reserves each class's run with one atomic (not one per wave:
+  // atomics on one counter serialise at the memory side, about 12.5 ns each,
+  // so fewer and larger workgroups reserve faster), and each wave takes its part
   // of the run in wave order, so a wave's (and the workgroup's) segments of
   // one class sit in consecutive positions in segment order
   // (classified-abi.md:56-66).
-  __shared__ long long run_s[4][kWavesPerBlock];
+  __shared__ long long run_s[4][kClassifyWaves];
   const int wave = threadIdx.x / kWave;
   uint64_t ballots[4];
 #pragma unroll
@@ -497,14 +499,14 @@ __global__ __launch_bounds__(kBlock) void k_classify(Params p) {
   if (threadIdx.x < 4) {
     const int c = threadIdx.x;
     long long total = 0;
-    for (int w = 0; w < kWavesPerBlock; ++w) total += run_s[c][w];
+    for (int w = 0; w < waves; ++w) total += run_s[c][w];
     // Run 3 is counted in counters[8]. A register-resident softmax
     // (block_items set) counts run 0 in counters[7]: k_softmax_deferred
     // takes the wave class, and k_softmax_fused, which reads counters[0],
     // sees none.
     const int slot = c == 3 ? 8 : c == 0 && p.block_items ? 7 : c;
     long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + slot), (unsigned long long)total) : 0;
-    for (int w = 0; w < kWavesPerBlock; ++w) {
+    for (int w = 0; w < waves; ++w) {
       const long long count = run_s[c][w];
       run_s[c][w] = base;
       base += count;
