@@ -364,6 +364,18 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   __shared__ int64_t stamp_s[5];    // item timeline (diagnostics), thread 0 only
   const int t = threadIdx.x;
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
+  // Rows of this thread inside an item: row0 + i * rstep. Where a row fits
+  // in one wave (lpr <= 64), each wave holds its own run of consecutive rows,
+  // so a wave's RPT loads read one contiguous span: on MI355X a 64 KiB item
+  // read as 4 KiB-strided 1 KiB pieces per wave moves 5.2 TB/s, read as one
+  // 16 KiB span per wave 6.05 TB/s (measured on a held-item copy). Wider rows
+  // keep one row per workgroup step.
+  const bool wave_rows = g.lpr <= kWave;
+  const int rstep = wave_rows ? kWave / g.lpr : g.rows_step;
+  const int row0 = wave_rows ? (t / kWave) * RPT * rstep + (t % kWave) / g.lpr : g.row_lane;
+  // First row of this wave (uniform): row groups wholly past the item are
+  // skipped per wave.
+  const int wave_row0 = wave_rows ? __builtin_amdgcn_readfirstlane((t / kWave) * RPT * rstep) : 0;
   // Ticket order: chunks of segments merged by tree (top of the item
   // array), chunks of segments merged directly (bottom), block-class
   // segments, wave-class segments (far end of block_items). k_classify
@@ -379,10 +391,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   const int64_t d = p.d;
   // Byte offsets inside an item: per thread, and the stride between a
   // thread's rows.
-  const int voff_in = g.active ? (g.row_lane * p.d + g.feature) * (int)sizeof(T) : kOutOfRange;
-  const int step_in = g.rows_step * p.d * (int)sizeof(T);
-  const int voff_mask = g.active ? (g.row_lane * p.d + g.feature) * 4 : kOutOfRange;
-  const int step_mask = g.rows_step * p.d * 4;
+  const int voff_in = g.active ? (row0 * p.d + g.feature) * (int)sizeof(T) : kOutOfRange;
+  const int step_in = rstep * p.d * (int)sizeof(T);
+  const int voff_mask = g.active ? (row0 * p.d + g.feature) * 4 : kOutOfRange;
+  const int step_mask = rstep * p.d * 4;
   // Index of a chunk ticket in the item (and pair) arrays.
   auto index_of = [&](int64_t ticket) -> int64_t {
     return ticket < n_tree ? p.items_cap - n_tree + ticket : ticket - n_tree;
@@ -457,10 +469,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     // the identity of the max and a zero mass.
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
-      if (!(g.active && g.row_lane < rows - i * g.rows_step)) Reg::fill_neg_inf(data[i]);
+      if (!(g.active && row0 < rows - i * rstep)) Reg::fill_neg_inf(data[i]);
     }
-    // Row groups wholly past the item (uniform) skip the arithmetic below.
-    auto live = [&](int i) { return i == 0 || i * g.rows_step < rows; };
+    // Row groups wholly past the item (wave-uniform) skip the arithmetic below.
+    auto live = [&](int i) { return i == 0 || wave_row0 + i * rstep < rows; };
     float m[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) m[v] = neg_inf();
@@ -512,7 +524,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     if (t == 0) stamp_s[2] = wall_clock64();
     // The item's column statistics leave registers for LDS: the merge below
     // then holds nothing but the rows.
-    if (g.row_lane == 0 && g.active) {
+    if (row0 == 0 && g.active) {
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
         own_m[g.feature + v] = m[v];
