@@ -189,7 +189,8 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
 
 /* Enqueue the plan on `stream` (a hipStream_t); replaces run_plan
  * (Driver.cpp:299-353). `workspace` must hold plan->workspace_bytes bytes
- * (may be NULL when that is 0); `mask` is NULL unless the module has one. */
+ * at a 256-byte aligned address (may be NULL when that is 0); `mask` is NULL
+ * unless the module has one. */
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
            void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
 

@@ -511,6 +511,8 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
   if (plan->workspace_bytes && (!workspace || workspace_bytes < plan->workspace_bytes))
     return fail(RG_E_WORKSPACE, "workspace of %llu bytes is smaller than the plan's %llu",
                 (unsigned long long)workspace_bytes, (unsigned long long)plan->workspace_bytes);
+  if (plan->workspace_bytes && ((uintptr_t)workspace & (kAlign - 1)) != 0)
+    return fail(RG_E_WORKSPACE, "workspace must be %llu-byte aligned", (unsigned long long)kAlign);
   rg::Params p;
   std::memset(&p, 0, sizeof p);
   p.values = values;

@@ -451,10 +451,17 @@ __global__ __launch_bounds__(kBlock) void k_init(Params p) {
     for (int64_t i = tid; i < p.b_split; i += threads) p.seg_arrive[i] = 0;
   }
   if (p.pairs) {
+    // Pair slots in 16-byte stores (two slots each; both arrays start
+    // 256-byte aligned), an odd last slot alone.
     const uint64_t sentinel = (uint64_t)kSentinel << 32;
-    const int64_t slots = p.items_cap * p.d;
-    for (int64_t i = tid; i < slots; i += threads) p.pairs[i] = sentinel;
-    for (int64_t i = tid; i < p.b_split * p.d; i += threads) p.final_pairs[i] = sentinel;
+    const ulonglong2 two = {sentinel, sentinel};
+    const int64_t slots = p.items_cap * p.d, final_slots = p.b_split * p.d;
+    ulonglong2* pairs2 = reinterpret_cast<ulonglong2*>(p.pairs);
+    ulonglong2* final2 = reinterpret_cast<ulonglong2*>(p.final_pairs);
+    for (int64_t i = tid; i < slots / 2; i += threads) pairs2[i] = two;
+    for (int64_t i = tid; i < final_slots / 2; i += threads) final2[i] = two;
+    if (tid == 0 && (slots & 1)) p.pairs[slots - 1] = sentinel;
+    if (tid == 0 && (final_slots & 1)) p.final_pairs[final_slots - 1] = sentinel;
     for (int64_t i = tid; i < p.items_cap; i += threads) p.arrive[i] = 0;
   }
 }

@@ -10,7 +10,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from gpu_helpers import check, run_program
+from gpu_helpers import check, quantized, run_program
 
 pytestmark = pytest.mark.gpu
 
@@ -18,7 +18,7 @@ torch = pytest.importorskip("torch")
 if not torch.cuda.is_available():  # pragma: no cover - CPU containers
     pytest.skip("no ROCm device", allow_module_level=True)
 
-from ragged import Compiler, Hints, Optimizations, ProgramSpec, native  # noqa: E402
+from ragged import Compiler, Hints, Optimizations, ProgramSpec, ValidationError, native  # noqa: E402
 from ragged.workloads import make_lengths, offsets_from_lengths  # noqa: E402
 
 _programs = {}
@@ -252,6 +252,34 @@ def test_wave_class_runs(artifact_cache, op, d, dtype):
     for c in range(3):
         np.testing.assert_array_equal(np.sort(ids[c, :counts[c]]), np.flatnonzero(classes == c))
     np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
+
+
+def test_misaligned_workspace_rejected(artifact_cache):
+    """rg_run takes the workspace at a 256-byte aligned address (its buffers
+    sit at 256-byte offsets and are filled with 16-byte stores): a shifted
+    pointer is rejected before any launch, the aligned one runs."""
+    program = program_for(artifact_cache, "softmax", "bf16", 128, "i64")
+    lengths = np.array([300, 5, 700, 0, 40], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    device = torch.device("cuda", 0)
+    values = torch.randn(int(offsets[-1]), 128, device=device).to(torch.bfloat16)
+    off = torch.from_numpy(offsets).to(device)
+    out = torch.full_like(values, -7)
+    module = program._module(0)
+    plan = program._plan(module, values.shape[0], len(lengths), "classified")
+    assert plan.workspace_bytes > 0
+    workspace = torch.empty(plan.workspace_bytes + 256, dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream().cuda_stream
+    with pytest.raises(ValidationError, match="aligned"):
+        module.run(plan, values.data_ptr(), off.data_ptr(), out.data_ptr(), None, workspace.data_ptr() + 16,
+                   plan.workspace_bytes, stream)
+    torch.cuda.synchronize()
+    assert bool(torch.all(out == -7)), "a rejected call wrote its output"
+    module.run(plan, values.data_ptr(), off.data_ptr(), out.data_ptr(), None, workspace.data_ptr(),
+               plan.workspace_bytes, stream)
+    torch.cuda.synchronize()
+    check(out.float().cpu().numpy().astype(np.float64), quantized(values.float().cpu().numpy(), "bf16"), offsets,
+          op="softmax", dtype="bf16")
 
 
 @pytest.mark.parametrize("op,dtype,d", [("sum", "f32", 1), ("max", "f32", 128), ("softmax", "f32", 1024),
