@@ -132,11 +132,11 @@ def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_
     if role == "init":
         return 0
     if role == "worker":
-        # The classified worker reads every row once; it writes every
-        # reduction result, or the softmax rows of unsplit segments (split
-        # segments' rows are written by split_normalize).
+        # The classified worker reads every row once and writes every
+        # reduction result, or every softmax row (split segments' rows after
+        # a re-read that is not algorithmic).
         if op == "softmax":
-            return (int(lengths.sum()) + int(lengths[lengths <= t_block].sum())) * d * element
+            return 2 * int(lengths.sum()) * d * element
         return (int(lengths.sum()) + len(lengths)) * d * element
     if role == "naive":
         rows = lengths

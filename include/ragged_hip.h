@@ -56,7 +56,7 @@ enum rg_role {
   RG_ROLE_BLOCK = 3,           /* not launched: the block class runs inside RG_ROLE_WORKER */
   RG_ROLE_SPLIT_PARTIAL = 4,   /* not launched: split parts run inside RG_ROLE_WORKER */
   RG_ROLE_SPLIT_COMBINE = 5,   /* not launched: the last part of a segment combines, inside RG_ROLE_WORKER */
-  RG_ROLE_SPLIT_NORMALIZE = 6, /* softmax: normalise each part */
+  RG_ROLE_SPLIT_NORMALIZE = 6, /* not launched: the classified worker normalises split parts */
   RG_ROLE_NAIVE = 7,           /* block-per-segment schedule */
   RG_ROLE_FUSED = 8,           /* softmax: register-resident worker over all block/split items */
   RG_ROLE_DEFERRED = 9,        /* softmax: re-read pass for chunks that stopped waiting, then the
@@ -127,7 +127,9 @@ enum rg_buffer {
   RG_BUF_COUNTERS = 0,      /* i64 slots: 0 wave-class segments of at most alone_rows rows, 1 block,
                                2 split counts, 3 split items, 4 work ticket, 5 deferred count,
                                6 tree items; 7 slot 0's count for a register-resident softmax
-                               (whose slot 0 stays 0); 8 the rest of the wave class; then 16
+                               (whose slot 0 stays 0); 8 the rest of the wave class; 9 softmax
+                               split-part normalisation ticket; 10 normalisation waits that
+                               ran out of their bound (0 unless something hung); then 16
                                ticket counters of the classified worker, 256 bytes apart from
                                byte 256 (4352 bytes in all) */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class; the wave class holds

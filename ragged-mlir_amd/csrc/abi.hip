@@ -248,7 +248,7 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
   module->roles[RG_ROLE_INIT] = rg::kernel_init();
   module->roles[RG_ROLE_CLASSIFY] = rg::kernel_classify(spec.offsets_dtype);
   module->roles[RG_ROLE_WORKER] = k.worker;
-  module->roles[RG_ROLE_SPLIT_NORMALIZE] = k.split_normalize;
+  // RG_ROLE_SPLIT_NORMALIZE stays empty: k_worker normalises split parts.
   module->roles[RG_ROLE_NAIVE] = k.naive;
   const bool f32_logits = spec.has_mask != 0 || spec.scale != 1.0f;
   const void* fused = f32_logits ? k.fused_f32 : k.fused;
@@ -492,10 +492,6 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   // a split part, a block segment or a batch of wave segments).
   const int64_t tickets = items_cap * tiles_block + b;
   add_launch(RG_ROLE_WORKER, std::min(module->resident[RG_ROLE_WORKER], std::max<int64_t>(tickets, 1)), 1);
-  if (b_split && softmax)
-    add_launch(RG_ROLE_SPLIT_NORMALIZE,
-               std::min(module->resident[RG_ROLE_SPLIT_NORMALIZE] / std::max<int64_t>(tiles_block, 1), items_cap),
-               tiles_block);
   return RG_OK;
 }
 
@@ -538,6 +534,9 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
   p.short_segments = plan->schedule == RG_SHORT_SEGMENTS ? 1 : 0;
   p.alone_rows = spec.alone_rows;
   if (plan->schedule == RG_CLASSIFIED) {
+    // A split part's wait for its segment's statistics ends by itself (see
+    // normalize_part); one second bounds it all the same.
+    p.drain_ticks = module->clock_khz * 1000;
     p.counters = static_cast<int64_t*>(buffer(RG_BUF_COUNTERS));
     p.queue = static_cast<int64_t*>(buffer(RG_BUF_QUEUE));
     p.item_pos = static_cast<int64_t*>(buffer(RG_BUF_ITEM_POS));

@@ -52,6 +52,7 @@ constexpr int kClassifyWaves = kClassifyBlock / kWave;
 constexpr int64_t kClassifyLarge = 16384;
 constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
+constexpr int32_t kStatsReady = -1;     // seg_arrive[k] once a split segment's softmax statistics are published
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
@@ -107,6 +108,7 @@ struct Params {
   uint64_t* pairs;         // [items_cap, D] published (m, s) of each chunk
   uint64_t* final_pairs;   // [B_split, D] merged (M, S) of long split segments
   int64_t spin_ticks;      // wall-clock ticks a chunk waits for its segment before deferring
+  int64_t drain_ticks;     // wall-clock bound of a split part's wait for its segment's statistics
   int64_t wait_parts;      // longest segment (in chunks) whose chunks wait for each other
   int64_t* trace;          // [trace_cap, 8] item timeline or null (diagnostics)
   int64_t trace_cap;

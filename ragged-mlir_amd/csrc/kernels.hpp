@@ -9,8 +9,8 @@
 //    (worker.hpp) drains the queues (ToGPU.cpp:999-1045). A split segment is
 //    cut into ceil(L / part_rows) parts -- proportional to its length instead
 //    of the reference's fixed 8 -- each processed by one workgroup; the last
-//    part folds them (ToGPU.cpp:399-472) and, for softmax,
-//    k_split_normalize writes the probabilities (ToGPU.cpp:279-281).
+//    part folds them (ToGPU.cpp:399-472) and, for softmax, the worker
+//    then writes the probabilities (ToGPU.cpp:279-281).
 #pragma once
 
 #include <type_traits>
@@ -398,38 +398,6 @@ __device__ __forceinline__ int combine_features(int d) {
   int f = 1;
   while (f < d && f < kCombineFeatures) f <<= 1;
   return f;
-}
-
-// Softmax normalisation of each split part with the combined statistics.
-template <int OP, class T, class OffT, int VEC, bool FLAT, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_split_normalize(Params p) {
-  const int64_t items = p.counters[3] < p.items_cap ? p.counters[3] : p.items_cap;
-  const int t = threadIdx.x;
-  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-    int64_t k, s, part, start, end;
-    item_rows<OffT>(p, item, k, s, part, start, end);
-    float m[VEC], inv[VEC];
-    if constexpr (FLAT) {
-#pragma unroll
-      for (int c = 0; c < VEC; ++c) {
-        const int f = c % p.d;
-        m[c] = p.stats_max[k * p.d + f];
-        inv[c] = 1.0f / p.stats_sum[k * p.d + f];
-      }
-      normalize_flat<T, VEC, MASK>(p, kBlock, t, start * p.d, end * p.d, m, inv);
-    } else {
-      const RowGeo g = row_geo<VEC>(p.d, kBlock, t, blockIdx.y);
-      if (g.active) {
-#pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          m[v] = p.stats_max[k * p.d + g.feature + v];
-          inv[v] = 1.0f / p.stats_sum[k * p.d + g.feature + v];
-        }
-        normalize_rows<T, VEC, MASK>(p, g, start, end, m, inv);
-      }
-    }
-    if (p.visits && part == 0 && blockIdx.y == 0 && t == 0) atomicAdd(p.visits + s, 1);
-  }
 }
 
 #ifdef RG_PROLOGUE_KERNELS

@@ -15,7 +15,6 @@ namespace rg {
 struct KernelSet {
   const void* naive;
   const void* worker;            // classified schedule: wave, block and split classes in one launch
-  const void* split_normalize;   // softmax only
   const void* fused;             // softmax, row mapping: register-resident worker
   const void* fused_f32;         // same, storing f32 logits (scale or mask on bf16 input)
   const void* deferred;          // softmax: re-read pass for chunks that stopped waiting
@@ -74,7 +73,6 @@ const void* kernel_offsets_check(int offsets_dtype);
 #define RG_SET(OP, T, OFFT, VEC, FLAT, MASK)                                              \
   {(const void*)&rg::k_naive<OP, T, OFFT, VEC, FLAT, MASK>,                               \
    (const void*)&rg::k_worker<OP, T, OFFT, VEC, FLAT, MASK>,                              \
-   OP == rg::OP_SOFTMAX ? (const void*)&rg::k_split_normalize<OP, T, OFFT, VEC, FLAT, MASK> : nullptr, \
    rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, std::is_same<T, float>::value>(),              \
    rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, true>(),                                       \
    rg::deferred_kernel<OP, T, OFFT, VEC, FLAT, MASK>(),                                          \
@@ -86,7 +84,7 @@ const void* kernel_offsets_check(int offsets_dtype);
 #define RG_GEOMETRIES(OP, OFFT, MASK)                                                           \
   {{RG_SET(OP, float, OFFT, 1, false, MASK), RG_SET(OP, float, OFFT, 2, false, MASK),          \
     RG_SET(OP, float, OFFT, 4, false, MASK), RG_SET(OP, float, OFFT, 4, true, MASK),           \
-    {nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                                      \
+    {nullptr, nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                                      \
    {RG_SET(OP, __bf16, OFFT, 1, false, MASK), RG_SET(OP, __bf16, OFFT, 2, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 4, false, MASK), RG_SET(OP, __bf16, OFFT, 8, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 8, true, MASK)}}

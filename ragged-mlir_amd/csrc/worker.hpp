@@ -9,9 +9,9 @@
 // address serialises atomics), longest work first:
 //   1. the parts of split segments; the part that arrives last at its
 //      segment's counter folds every part in part order (deterministic) and
-//      writes the result (sum, max) or the merged statistics (softmax, then
-//      normalised by k_split_normalize) -- the reference's split_combine
-//      (ToGPU.cpp:399-472) without a separate launch;
+//      writes the result (sum, max) or the merged statistics (softmax) --
+//      the reference's split_combine (ToGPU.cpp:399-472) without a separate
+//      launch;
 //   2. block-class segments, one workgroup each;
 //   3. wave-class segments longer than alone_rows, one wave each (queued
 //      from the back of the wave queue);
@@ -19,6 +19,9 @@
 //      reduced alone by one lane (flat mapping, D below the vector width) or
 //      by the group of lanes that holds a row -- a batch costs one pass of
 //      the wave instead of one wave-wide reduction per segment.
+// Softmax, once a workgroup's tickets run out: the split parts'
+// probabilities (the reference's split_normalize, ToGPU.cpp:279-281), from
+// a counter of their own, each after its segment's statistics are out.
 // The short-segment schedule runs only step 4, over every segment in order.
 #pragma once
 
@@ -411,8 +414,8 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
     if (pl == 0 && f < p.d) {
       for (int q = 1; q < pl_count; ++q) acc.merge(st_read<OP>(lds + q * ft + fl, kBlock));
       if constexpr (OP == OP_SOFTMAX) {
-        p.stats_max[k * p.d + f] = acc.m;
-        p.stats_sum[k * p.d + f] = acc.s;
+        publish(p.stats_max + k * p.d + f, acc.m);
+        publish(p.stats_sum + k * p.d + f, acc.s);
       } else {
         Elem<T>::put(static_cast<T*>(p.out) + s * p.d + f, value_of<OP>(acc));
       }
@@ -421,7 +424,58 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
   }
   if constexpr (OP != OP_SOFTMAX) {
     if (p.visits && t == 0) atomicAdd(p.visits + s, 1);
+  } else {
+    // The statistics are complete once every thread's stores are: release
+    // the segment's parts to their normalisation (normalize_part).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    if (t == 0) __hip_atomic_store(p.seg_arrive + k, kStatsReady, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// Softmax probabilities of split part `item` (feature tile `tile`) with its
+// segment's combined statistics (ToGPU.cpp:279-281), once the segment's last
+// part has published them. The wait ends: every part was handed to a running
+// workgroup before any workgroup gets here, and a part never waits. A
+// wall-clock bound (drain_ticks) guards against a hang all the same; running
+// out of it is counted in counters[10].
+template <class T, class OffT, int VEC, bool FLAT, bool MASK>
+__device__ __forceinline__ void normalize_part(const Params& p, int64_t item, int tile) {
+  const int t = threadIdx.x;
+  int64_t k, s, part, start, end;
+  item_rows<OffT>(p, item, k, s, part, start, end);
+  if (t == 0) {
+    const long long t0 = wall_clock64();
+    while (__hip_atomic_load(p.seg_arrive + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != kStatsReady) {
+      if (wall_clock64() - t0 >= p.drain_ticks) {
+        atomicAdd((unsigned long long*)(p.counters + 10), 1ull);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+  float m[VEC], inv[VEC];
+  if constexpr (FLAT) {
+#pragma unroll
+    for (int c = 0; c < VEC; ++c) {
+      const int f = c % p.d;
+      m[c] = fetch(p.stats_max + k * p.d + f);
+      inv[c] = 1.0f / fetch(p.stats_sum + k * p.d + f);
+    }
+    normalize_flat<T, VEC, MASK>(p, kBlock, t, start * p.d, end * p.d, m, inv);
+  } else {
+    const RowGeo g = row_geo<VEC>(p.d, kBlock, t, tile);
+    if (g.active) {
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) {
+        m[v] = fetch(p.stats_max + k * p.d + g.feature + v);
+        inv[v] = 1.0f / fetch(p.stats_sum + k * p.d + g.feature + v);
+      }
+      normalize_rows<T, VEC, MASK>(p, g, start, end, m, inv);
+    }
+  }
+  if (p.visits && part == 0 && tile == 0 && t == 0) atomicAdd(p.visits + s, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -540,6 +594,23 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
       coop_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - n_parts - n_block, n_coop);
     } else {
       wave_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - before_alone, n_wave, direct);
+    }
+  }
+  // Softmax: the split parts' probabilities, from a counter of their own,
+  // once this workgroup's tickets have run out (so every part has been
+  // handed out).
+  if constexpr (OP == OP_SOFTMAX) {
+    if (n_parts > 0) {
+      for (;;) {
+        __syncthreads();
+        if (t == 0) ticket_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 9), 1ull);
+        __syncthreads();
+        const int64_t i = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)ticket_s >> 32))
+                                     << 32) |
+                                    __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)ticket_s));
+        if (i >= n_parts) break;
+        normalize_part<T, OffT, VEC, FLAT, MASK>(p, i / tiles_block, (int)(i % tiles_block));
+      }
     }
   }
 }

@@ -46,10 +46,8 @@ def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> 
     if fused:
         return roles + ["fused_online", "deferred_online"]
     # One persistent worker drains every class; the reference's per-class
-    # chains and split combine run inside it.
+    # chains, split combine and (softmax) split normalisation run inside it.
     roles.append(f"worker_{phase}")
-    if "split" in classes and spec.op == "softmax":
-        roles.append("split_normalize")
     return roles
 
 

@@ -254,6 +254,35 @@ def test_wave_class_runs(artifact_cache, op, d, dtype):
     np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
 
 
+@pytest.mark.parametrize("d,dtype,masked", [(1, "f32", False), (2, "f32", True), (4, "bf16", False), (1, "bf16", True)])
+def test_softmax_split_parts_normalised_by_worker(artifact_cache, d, dtype, masked):
+    """Softmax with many split segments of several parts each (streaming
+    worker geometries): the worker normalises every part once its segment's
+    statistics are out; exact results, every segment written once, and no
+    separate normalisation launch."""
+    spec = native.make_spec("softmax", dtype, "i64", d)
+    t_block, part_rows = spec.t_block, spec.part_rows
+    rng = np.random.default_rng(41 + d)
+    long = rng.integers(t_block + 1, t_block + 2 * part_rows, size=8)
+    lengths = rng.permutation(np.concatenate([long, rng.integers(0, 300, size=3000), [t_block + 1]]))
+    lengths = lengths.astype(np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    kwargs = dict(mask=True, scale=0.75) if masked else {}
+    mask = np.where(rng.random(values.shape) < 0.1, -np.inf, rng.normal(size=values.shape)).astype(np.float32) \
+        if masked else None
+    program = program_for(artifact_cache, "softmax", dtype, d, "i64", **kwargs)
+    actual, report = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified", mask=mask)
+    assert "split_normalize" not in " ".join(report.kernel_names)
+    check(actual, values, offsets, op="softmax", dtype=dtype, mask=mask, scale=0.75 if masked else 1.0)
+    debug = program_for(artifact_cache, "softmax", dtype, d, "i64", debug_visits=True, **kwargs)
+    buffers = {}
+    actual, _ = run_program(debug, values, offsets, dtype=dtype, op="softmax", mask=mask, debug_buffers=buffers)
+    check(actual, values, offsets, op="softmax", dtype=dtype, mask=mask, scale=0.75 if masked else 1.0)
+    assert int(buffers["class_counts"].cpu().numpy()[2]) == int((lengths > t_block).sum())
+    np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
+
+
 def test_misaligned_workspace_rejected(artifact_cache):
     """rg_run takes the workspace at a 256-byte aligned address (its buffers
     sit at 256-byte offsets and are filled with 16-byte stores): a shifted
