@@ -32,6 +32,9 @@ _modules: dict[tuple[int, str], native.NativeModule] = {}   # (device, artifact 
 _device_arch: dict[int, str] = {}
 _device_runs: dict[tuple[int, str], bool] = {}     # (device, chip) -> the chip's code runs there
 _device_l2_mib: dict[int, float | None] = {}
+# torch.cuda.Stream objects of current streams, keyed by torch's exact
+# (stream id, device index, device type) of each: equal keys are one stream.
+_current_streams: dict[tuple, Any] = {}
 I64_MAX = 2**63 - 1
 
 
@@ -64,11 +67,26 @@ def device_l2_mib(values) -> float | None:
     return _device_l2_mib[index]
 
 
-def _overlaps(left, right) -> bool:
-    lstart, rstart = left.data_ptr(), right.data_ptr()
-    lend = lstart + left.numel() * left.element_size()
-    rend = rstart + right.numel() * right.element_size()
-    return lstart < rend and rstart < lend
+def _span(tensor) -> tuple[int, int]:
+    """[first byte, one past the last byte) of a contiguous tensor."""
+    start = tensor.data_ptr()
+    return start, start + tensor.numel() * tensor.element_size()
+
+
+def _spans_overlap(left: tuple[int, int], right: tuple[int, int]) -> bool:
+    return left[0] < right[1] and right[0] < left[1]
+
+
+def _current_stream(torch, device: int):
+    """torch.cuda.current_stream(device), without building a new Stream
+    object per call."""
+    key = torch._C._cuda_getCurrentStream(device)
+    stream = _current_streams.get(key)
+    if stream is None:
+        if len(_current_streams) > 64:
+            _current_streams.clear()
+        stream = _current_streams[key] = torch.cuda.Stream(stream_id=key[0], device_index=key[1], device_type=key[2])
+    return stream
 
 
 class CompiledProgram:
@@ -96,6 +114,8 @@ class CompiledProgram:
         self._workspaces: dict[tuple[int, int], Any] = {}
         self._names = {kernel["role"]: kernel["name"] for kernel in self._metadata["kernels"]}
         self._alone: int | None = None
+        self._torch_dtypes: tuple | None = None    # (values dtype, offsets dtype) as torch dtypes
+        self._report_static: tuple | None = None   # (classes, thresholds) of every report
 
     @property
     def selects(self) -> bool:
@@ -169,8 +189,11 @@ class CompiledProgram:
             raise ValidationError("values must have shape [N, static D]")
         if offsets.ndim != 1 or offsets.numel() < 1:
             raise ValidationError("offsets must have shape [B+1], including [0] when B=0")
-        dtype = {"f32": torch.float32, "bf16": torch.bfloat16}[self.spec.dtype]
-        offset_dtype = {"i32": torch.int32, "i64": torch.int64}[self.spec.offsets_dtype]
+        dtypes = self._torch_dtypes
+        if dtypes is None:
+            dtypes = self._torch_dtypes = ({"f32": torch.float32, "bf16": torch.bfloat16}[self.spec.dtype],
+                                           {"i32": torch.int32, "i64": torch.int64}[self.spec.offsets_dtype])
+        dtype, offset_dtype = dtypes
         if values.dtype != dtype or out.dtype != dtype or offsets.dtype != offset_dtype:
             raise ValidationError("tensor dtype differs from compiled dtype/offsets specialization")
         vector = self._metadata["d_vector"]
@@ -192,18 +215,20 @@ class CompiledProgram:
         expected = (n if self.spec.op == "softmax" else b, self.spec.feature_dim)
         if tuple(out.shape) != expected:
             raise ValidationError(f"out shape must be {expected}")
+        values_span, offsets_span, out_span = _span(values), _span(offsets), _span(out)
         if mask is not None:
             if mask.dtype != torch.float32 or tuple(mask.shape) != tuple(values.shape):
                 raise ValidationError("mask must have f32 dtype and exactly values shape [N,D]; "
                                       "broadcasting is unsupported")
             if mask.device != values.device:
                 raise ValidationError("mask must use the values device")
-            if _overlaps(mask, out) or _overlaps(mask, offsets):
+            mask_span = _span(mask)
+            if _spans_overlap(mask_span, out_span) or _spans_overlap(mask_span, offsets_span):
                 raise ValidationError("mask must not overlap out or offsets")
-        if _overlaps(offsets, values) or _overlaps(offsets, out):
+        if _spans_overlap(offsets_span, values_span) or _spans_overlap(offsets_span, out_span):
             raise ValidationError("offsets must not alias values or out")
-        overlap = values.numel() and out.numel() and _overlaps(values, out)
-        exact = values.data_ptr() == out.data_ptr() and tuple(values.shape) == tuple(out.shape)
+        overlap = values.numel() and out.numel() and _spans_overlap(values_span, out_span)
+        exact = values_span[0] == out_span[0] and values.shape == out.shape
         if overlap:
             if not exact or self.spec.alias != "inplace" or not self._metadata["alias_safe"]:
                 raise ValidationError("out aliases values without a safe in-place schedule")
@@ -299,8 +324,11 @@ class CompiledProgram:
     def _report(self, started, plan_names=(), grids=(), workspace=0, *, mode, selected, selection,
                 validation_bytes=0, validation_ms=None) -> ExecutionReport:
         metadata = self._metadata
+        static = self._report_static
+        if static is None:
+            static = self._report_static = (tuple(metadata["classes"]), tuple(metadata["thresholds"]))
         return ExecutionReport(
-            tuple(metadata["classes"]) if plan_names else (), tuple(metadata["thresholds"]), tuple(grids),
+            static[0] if plan_names else (), static[1], tuple(grids),
             workspace + validation_bytes, self._digest, None, mode, tuple(plan_names),
             (time.perf_counter() - started) * 1000, cache_hit=self.cache_hit,
             validation_workspace_bytes=validation_bytes, validation_host_ms=validation_ms,
@@ -344,9 +372,12 @@ class CompiledProgram:
             if not runs:
                 raise RuntimeUnavailable(f"compiled target {self.spec.chip} does not run on the current device "
                                          f"({_device_arch[device]})")
-            active = stream if stream is not None else torch.cuda.current_stream(device)
-            if not isinstance(active, torch.cuda.Stream) or active.device != values.device:
-                raise ValidationError("stream must be a torch.cuda.Stream on the values device")
+            if stream is None:
+                active = _current_stream(torch, device)
+            else:
+                active = stream
+                if not isinstance(active, torch.cuda.Stream) or active.device != values.device:
+                    raise ValidationError("stream must be a torch.cuda.Stream on the values device")
             module = self._module(device)
             names, grids, validation_bytes, validation_ms = [], [], 0, None
             if checked:
