@@ -18,10 +18,16 @@ Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
   within 3% of the faster schedule.
 * ``evaluate`` reports, for a suite's measurements, how many choices fall
   within 3% of the faster measured schedule.
+* ``transfer`` (the reference's ``calibrate.py transfer``, :229-272) takes
+  the train and held-out measurements of another device (or ROCm, or
+  firmware), refits there (written to ``--out``) and reports on its
+  held-out cases the shipped model, the shipped model given that device's
+  L2 capacity (``measure`` records it) and the refitted one.
 
     python -m ragged.calibrate measure --suite train --out train.jsonl
     python -m ragged.calibrate fit train.jsonl --out cost_model.json [--heldout heldout.jsonl]
     python -m ragged.calibrate evaluate heldout.jsonl [--model cost_model.json]
+    python -m ragged.calibrate transfer train.jsonl heldout.jsonl --out refit.json [--model cost_model.json]
 """
 from __future__ import annotations
 
@@ -120,8 +126,11 @@ def measure(cases: list[Case], out: Path, *, log=print) -> int:
         for line in out.read_text().splitlines():
             if line.strip():
                 done.add(json.loads(line)["key"])
+    from .runtime import device_l2_mib
+
     device = torch.device("cuda", 0)
     generator = torch.Generator(device=device)
+    l2_mib = device_l2_mib(torch.empty(1, device=device))   # recorded for `transfer`
     programs: dict[tuple, object] = {}
     cache = ArtifactCache(tempfile.mkdtemp(prefix="ragged-calibrate-"))
     measured = 0
@@ -148,7 +157,7 @@ def measure(cases: list[Case], out: Path, *, log=print) -> int:
                 run()
                 times[schedule] = round(_time_calls(torch, run), 2)
             record = {**asdict(case), "key": case.key, "max_len": max_len, "fused": bool(program.metadata["fused"]),
-                      "mapping": program.metadata["mapping"], "us": times}
+                      "mapping": program.metadata["mapping"], "l2_mib": l2_mib, "us": times}
             sink.write(json.dumps(record) + "\n")
             sink.flush()
             measured += 1
@@ -218,21 +227,25 @@ def fit_family(records: list[dict], schedule: str) -> tuple[np.ndarray, float]:
     return _fit_relative(rows, times, every), error
 
 
-def choices(model: CostModel, records: list[dict]) -> list[tuple[dict, str]]:
+def choices(model: CostModel, records: list[dict], device_l2: bool = False) -> list[tuple[dict, str]]:
+    """The model's schedule for every record; with ``device_l2``, given the
+    L2 capacity the record was measured with (when it holds one) instead of
+    the model's own."""
     out = []
     for record in records:
         element = 2 if record["dtype"] == "bf16" else 4
+        l2_mib = record.get("l2_mib") if device_l2 else None
         chosen, _ = model.choose(record["op"], record["n"], record["b"], record["d"], record["max_len"], element,
-                                 fused=bool(record.get("fused", False)), flat=_flat(record))
+                                 l2_mib=l2_mib, fused=bool(record.get("fused", False)), flat=_flat(record))
         out.append((record, chosen))
     return out
 
 
-def evaluate(model: CostModel, records: list[dict]) -> dict:
+def evaluate(model: CostModel, records: list[dict], device_l2: bool = False) -> dict:
     """Share of choices within 3% of the faster measured schedule, overall
     and per family, with the slowdown of every miss."""
     good, misses, per_family = 0, [], {f: [0, 0] for f in FAMILIES}
-    for record, chosen in choices(model, records):
+    for record, chosen in choices(model, records, device_l2):
         times = record["us"]
         best = min(times.values())
         ok = times[chosen] <= best * (1 + WITHIN)
@@ -279,6 +292,22 @@ def fit(records: list[dict]) -> dict:
     return data
 
 
+def transfer(train: list[dict], heldout: list[dict], shipped: CostModel) -> tuple[dict, dict]:
+    """(refitted model file, report): the refit on ``train`` and, on
+    ``heldout``, the share within 3% of the faster schedule for the shipped
+    model, the shipped model with the measured L2 capacity, and the refit
+    (reference bench/calibrate.py:229-272)."""
+    data = fit(train)
+    refit = CostModel.from_dict(data)
+    variants = {"shipped": evaluate(shipped, heldout), "shipped_device_l2": evaluate(shipped, heldout, True),
+                "refitted": evaluate(refit, heldout, True)}
+    l2 = sorted({r["l2_mib"] for r in heldout if r.get("l2_mib")})
+    report = {"heldout_cases": len(heldout), "device_l2_mib": l2, "shipped_l2_mib": shipped.l2_mib,
+              "train_within_3pct": data["calibration"]["train_within_3pct"],
+              **{name: {k: v for k, v in r.items() if k != "misses"} for name, r in variants.items()}}
+    return data, report
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = parser.add_subparsers(dest="command", required=True)
@@ -293,6 +322,11 @@ def main(argv=None) -> int:
     e = sub.add_parser("evaluate")
     e.add_argument("results", type=Path)
     e.add_argument("--model", type=Path)
+    t = sub.add_parser("transfer", help="the shipped model on another device's measurements, and refitted there")
+    t.add_argument("train", type=Path)
+    t.add_argument("heldout", type=Path)
+    t.add_argument("--out", type=Path, required=True, help="where to write the refitted model")
+    t.add_argument("--model", type=Path)
     args = parser.parse_args(argv)
     if args.command == "measure":
         cases = suite(args.suite)[: args.limit]
@@ -310,6 +344,13 @@ def main(argv=None) -> int:
             data["calibration"]["heldout_within_3pct"] = report["share"]
         args.out.write_text(json.dumps(data, indent=2) + "\n")
         print(json.dumps(data["calibration"], indent=2))
+        return 0
+    if args.command == "transfer":
+        shipped = CostModel.load(args.model) if args.model else CostModel.load()
+        data, report = transfer(load(args.train), load(args.heldout), shipped)
+        data["calibration"]["train_file"] = args.train.name
+        args.out.write_text(json.dumps(data, indent=2) + "\n")
+        print(json.dumps(report, indent=2))
         return 0
     model = CostModel.load(args.model) if args.model else CostModel.load()
     report = evaluate(model, load(args.results))

@@ -96,3 +96,45 @@ def test_shipped_model_meets_the_heldout_target():
         for schedule, coefficients in schedules.items():
             assert coefficients == pytest.approx(list(model.coefficients[fam][schedule]), rel=1e-4, abs=1e-6)
     assert refit["margin"] == model.margin
+
+
+def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp_path):
+    """`transfer` (reference bench/calibrate.py:229-272) refits on another
+    device's train measurements: run on the measurements the shipped model
+    was fitted on, its refit equals the shipped model and scores the same
+    held-out share; the CLI writes the refit and prints the report."""
+    directory = Path(calibrate.__file__).with_name("calibration")
+    train = calibrate.load(directory / "train.jsonl")
+    heldout = calibrate.load(directory / "heldout.jsonl")
+    shipped = CostModel.load()
+    data, report = calibrate.transfer(train, heldout, shipped)
+    assert data["coefficients"] == json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())[
+        "coefficients"]
+    assert data["margin"] == shipped.margin
+    assert report["shipped"]["within_3pct"] == report["refitted"]["within_3pct"] == 137
+    assert report["heldout_cases"] == 150
+    out = tmp_path / "refit.json"
+    assert calibrate.main(["transfer", str(directory / "train.jsonl"), str(directory / "heldout.jsonl"),
+                           "--out", str(out)]) == 0
+    assert json.loads(out.read_text())["coefficients"] == data["coefficients"]
+
+
+def test_transfer_gives_the_device_l2_to_the_shipped_model():
+    """The "shipped with the device's L2" variant passes each record's
+    measured L2 capacity to the model; records without one keep the model's."""
+    shipped = CostModel.load()
+    record = {"op": "sum", "dtype": "f32", "d": 128, "n": 1 << 22, "b": 4096, "distribution": "uniform",
+              "seed": 1, "key": "k", "max_len": 2048, "fused": False, "mapping": "row",
+              "us": {"classified": 100.0, "naive": 100.0}}
+    seen = []
+
+    class Spy(CostModel):
+        def choose(self, *args, **kwargs):
+            seen.append(kwargs.get("l2_mib"))
+            return super().choose(*args, **kwargs)
+
+    spy = Spy.from_dict(json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text()))
+    calibrate.evaluate(spy, [record, {**record, "l2_mib": 8.0}], device_l2=True)
+    calibrate.evaluate(spy, [{**record, "l2_mib": 8.0}])
+    assert seen == [None, 8.0, None]
+    assert shipped.l2_mib == 32.0
