@@ -111,8 +111,9 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     assert data["coefficients"] == json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())[
         "coefficients"]
     assert data["margin"] == shipped.margin
-    assert report["shipped"]["within_3pct"] == report["refitted"]["within_3pct"] == 137
     assert report["heldout_cases"] == 150
+    recorded = round(shipped.calibration["heldout_within_3pct"] * 150)
+    assert report["shipped"]["within_3pct"] == report["refitted"]["within_3pct"] == recorded
     out = tmp_path / "refit.json"
     assert calibrate.main(["transfer", str(directory / "train.jsonl"), str(directory / "heldout.jsonl"),
                            "--out", str(out)]) == 0
