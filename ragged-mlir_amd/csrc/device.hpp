@@ -39,7 +39,8 @@ constexpr int kCombineFeatures = 64;   // consecutive features per split-combine
 constexpr int kLaneElems = 64;         // classified worker: flat elements one lane reduces alone
 constexpr int kGroupRows = 32;         // classified worker: rows one lane group walks alone
 // The classified worker's work tickets come from kTicketLanes counters,
-// kTicketStride i64 (256 bytes) apart after the eight class counters:
+// kTicketStride i64 (256 bytes) apart, after the first kTicketStride slots
+// (the class counts and the other per-call counters):
 // atomics on one address serialise at about 12.5 ns each on MI355X, on 16
 // addresses at about 1 ns per ticket.
 constexpr int kTicketLanes = 16;
@@ -88,10 +89,13 @@ struct Params {
   int64_t part_rows;       // rows per split part
   int64_t items_cap;       // capacity of the split item tables
   int64_t b_split;         // capacity of the split queue / statistics rows
-  int64_t* counters;       // [8]: wave, block, split segment counts; split items;
-                           //      work ticket; deferred chunks; tree items; wave
-                           //      count of a register-resident softmax; then
-                           //      the worker's ticket lanes (kTicketStride apart)
+  int64_t* counters;       // slots 0-10: wave (reduced alone), block, split segment
+                           //      counts; split items; work ticket; deferred
+                           //      chunks; tree items; the wave count of a
+                           //      register-resident softmax; the rest of the wave
+                           //      class; the split-part normalisation ticket;
+                           //      normalisation waits past their bound. Then the
+                           //      worker's ticket lanes (kTicketStride apart)
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item
   int64_t* part_begin;     // [B] first item of each split-queue position
