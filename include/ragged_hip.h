@@ -125,13 +125,14 @@ typedef struct rg_plan {
 /* Workspace buffer indices (rg_plan.buffer_offset / buffer_bytes). */
 enum rg_buffer {
   RG_BUF_COUNTERS = 0,      /* i64 slots: 0 wave-class segments of at most alone_rows rows, 1 block,
-                               2 split counts, 3 split items, 4 work ticket, 5 deferred count,
-                               6 tree items; 7 slot 0's count for a register-resident softmax
-                               (whose slot 0 stays 0); 8 the rest of the wave class; 9 softmax
-                               split-part normalisation ticket; 10 normalisation waits that
-                               ran out of their bound (0 unless something hung); then 16
-                               ticket counters of the classified worker, 256 bytes apart from
-                               byte 256 (4352 bytes in all) */
+                               2 split counts, 3 split items, 4 work ticket, 5 deferred count
+                               (register-resident softmax chunks, or worker softmax split
+                               parts), 6 tree items; 7 slot 0's count for a register-resident
+                               softmax (whose slot 0 stays 0); 8 the rest of the wave class;
+                               9 softmax split-part normalisation ticket; 10 unused; 11 worker
+                               softmax workgroups finished; then 16 ticket counters of the
+                               classified worker, 256 bytes apart from byte 256 (4352 bytes
+                               in all) */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class; the wave class holds
                                its segments of at most alone_rows rows from the front and the
                                others from the back */
@@ -142,7 +143,9 @@ enum rg_buffer {
   RG_BUF_STATS_MAX = 6,     /* f32[B_split, D] (softmax) */
   RG_BUF_STATS_SUM = 7,     /* f32[B_split, D] (softmax) */
   RG_BUF_VISITS = 8,        /* i32[B] (debug_visits) */
-  RG_BUF_DEFERRED = 9,      /* i64[items_cap] chunks left to the re-read pass (fused softmax) */
+  RG_BUF_DEFERRED = 9,      /* i64[items_cap] chunks left to the re-read pass (fused softmax);
+                               i64[items_cap * feature tiles] split parts left to the worker's
+                               last workgroup (worker softmax) */
   RG_BUF_ARRIVE = 10,       /* i32[items_cap] chunk arrivals per 32-chunk group (fused softmax) */
   RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] part (fused softmax: group) arrivals per split segment */
   RG_BUF_ITEMS = 12,        /* 32-byte descriptors [items_cap] of split chunks (fused softmax) */
@@ -196,10 +199,14 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
            void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
 
-/* Longest wait, in microseconds, of a softmax chunk for the rest of its
- * segment before it defers to the re-read pass (default 2000). A test and
- * diagnostics control: 0 makes every chunk that finds its segment
- * unfinished take the re-read path. */
+/* Longest wait, in microseconds, of every softmax wait for statistics that
+ * other workgroups publish, before the work is deferred: a register-resident
+ * chunk's wait for the rest of its segment (default 2000; deferred chunks
+ * are re-read by RG_ROLE_DEFERRED) and a streaming worker split part's wait
+ * for its segment's statistics (default 1000000; deferred parts are
+ * normalised by the worker's last workgroup). Results do not depend on it.
+ * A test and diagnostics control: 0 makes every such wait that does not
+ * succeed at once take the deferred path; -1 restores both defaults. */
 int rg_module_set_spin_limit(rg_module* module, int64_t microseconds);
 
 /* Diagnostics: a timeline of the register-resident softmax's work items.

@@ -27,6 +27,7 @@ Pinning (what fails if the restatement is wrong):
 
 from .offsets import CONDITIONS, offsets_errors
 from .reference import (
+    Expectation,
     STRICT_TOLERANCES,
     TOLERANCES,
     assert_matches,
@@ -43,7 +44,7 @@ from .reference import (
 from .masked import assert_masked_softmax_matches, masked_logits
 
 __all__ = [
-    "STRICT_TOLERANCES",
+    "Expectation", "STRICT_TOLERANCES",
     "TOLERANCES", "assert_matches", "quantize_bf16", "segment_max", "segment_max_loop",
     "segment_reduce", "segment_softmax", "segment_softmax_loop", "segment_sum", "segment_sum_loop",
     "validate_offsets", "masked_logits", "assert_masked_softmax_matches", "CONDITIONS", "offsets_errors",

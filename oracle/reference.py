@@ -182,6 +182,78 @@ def segment_softmax_loop(values, offsets):
     return out
 
 
+class Expectation:
+    """The float64 reference of one (values, offsets, operation, dtype),
+    computed once and compared with any number of outputs.
+
+    ``check`` is the accuracy contract of oracle/reference.py:109-174 and
+    docs/semantics.md:69-88 (see ``assert_matches``, which is one
+    ``Expectation(...).check(...)``).
+    """
+
+    def __init__(self, values: np.ndarray, offsets: np.ndarray, *, operation: str, input_dtype: str):
+        functions = {"sum": segment_sum, "max": segment_max, "softmax": segment_softmax}
+        if operation not in functions:
+            raise ValueError("operation must be sum, max, or softmax")
+        if input_dtype not in TOLERANCES:
+            raise ValueError("input_dtype must be f32 or bf16")
+        self.operation, self.input_dtype = operation, input_dtype
+        self.offsets = np.asarray(offsets)
+        reference = functions[operation](values, offsets)
+        with np.errstate(over="ignore", invalid="ignore"):
+            rounded = reference.astype(np.float32)
+            if input_dtype == "bf16":
+                rounded = quantize_bf16(rounded)
+        # Where rounding the reference to the output dtype overflows, the
+        # signed infinity is expected instead.
+        self.expected = np.where(np.isinf(rounded), rounded.astype(np.float64), reference)
+        self.scale = segment_sum(np.abs(values), offsets) if operation == "sum" else np.abs(self.expected)
+        self.finite = np.isfinite(self.expected)
+
+    def check(self, actual: np.ndarray, tolerances: dict[str, tuple[float, float]] = TOLERANCES
+              ) -> dict[str, float | int]:
+        operation, input_dtype, expected, finite = self.operation, self.input_dtype, self.expected, self.finite
+        if input_dtype not in tolerances:
+            raise ValueError("input_dtype must be f32 or bf16")
+        actual = np.asarray(actual, dtype=np.float64)
+        if actual.shape != expected.shape:
+            raise AssertionError(f"shape mismatch: {actual.shape} != {expected.shape}")
+        if not np.array_equal(np.isnan(actual), np.isnan(expected)):
+            raise AssertionError("NaN locations differ from oracle")
+        if not np.array_equal(np.isposinf(actual), np.isposinf(expected)):
+            raise AssertionError("positive infinity locations differ from oracle")
+        if not np.array_equal(np.isneginf(actual), np.isneginf(expected)):
+            raise AssertionError("negative infinity locations differ from oracle")
+        rtol, atol = tolerances[input_dtype]
+        error = np.abs(actual[finite] - expected[finite])
+        bound = atol + rtol * self.scale[finite]
+        failures = error > bound
+        if np.any(failures):
+            raise AssertionError(
+                f"{operation}/{input_dtype}: {int(np.sum(failures))} finite values exceed "
+                f"tolerance; max abs error={float(np.max(error)):.9g}")
+        if operation == "softmax":
+            if np.any(actual[finite] < 0) or np.any(actual[finite] > 1):
+                raise AssertionError("finite softmax probabilities must lie in [0, 1]")
+            offsets64 = self.offsets.astype(np.int64)
+            lengths, mask, starts = _nonempty(offsets64)
+            if starts.size:
+                lo, hi = int(starts[0]), int(offsets64[-1])
+                # Per segment and column: is every expected entry finite, and
+                # the float64 column total of the actual output.
+                valid = np.logical_and.reduceat(finite[lo:hi], starts - lo, axis=0)
+                with np.errstate(invalid="ignore"):
+                    totals = np.add.reduceat(np.where(finite, actual, 0.0)[lo:hi], starts - lo, axis=0)
+                if np.any(np.abs(totals[valid] - 1) > rtol + atol):
+                    raise AssertionError("finite softmax columns must sum to one within dtype tolerance")
+        return {
+            "finite_values": int(np.sum(finite)),
+            "nan_values": int(np.sum(np.isnan(expected))),
+            "max_abs_error": float(np.max(error, initial=0)),
+            "max_fraction_of_tolerance": float(np.max(error / bound, initial=0)),
+        }
+
+
 def assert_matches(actual: np.ndarray, values: np.ndarray, offsets: np.ndarray, *,
                    operation: str, input_dtype: str,
                    tolerances: dict[str, tuple[float, float]] = TOLERANCES) -> dict[str, float | int]:
@@ -199,53 +271,6 @@ def assert_matches(actual: np.ndarray, values: np.ndarray, offsets: np.ndarray, 
     Returns the reference's error statistics. ``tolerances`` replaces the
     reference's (rtol, atol) table, e.g. with STRICT_TOLERANCES.
     """
-    functions = {"sum": segment_sum, "max": segment_max, "softmax": segment_softmax}
-    if operation not in functions:
-        raise ValueError("operation must be sum, max, or softmax")
     if input_dtype not in tolerances:
         raise ValueError("input_dtype must be f32 or bf16")
-    reference = functions[operation](values, offsets)
-    with np.errstate(over="ignore", invalid="ignore"):
-        rounded = reference.astype(np.float32)
-        if input_dtype == "bf16":
-            rounded = quantize_bf16(rounded)
-    expected = np.where(np.isinf(rounded), rounded.astype(np.float64), reference)
-    actual = np.asarray(actual, dtype=np.float64)
-    if actual.shape != expected.shape:
-        raise AssertionError(f"shape mismatch: {actual.shape} != {expected.shape}")
-    if not np.array_equal(np.isnan(actual), np.isnan(expected)):
-        raise AssertionError("NaN locations differ from oracle")
-    if not np.array_equal(np.isposinf(actual), np.isposinf(expected)):
-        raise AssertionError("positive infinity locations differ from oracle")
-    if not np.array_equal(np.isneginf(actual), np.isneginf(expected)):
-        raise AssertionError("negative infinity locations differ from oracle")
-    scale = segment_sum(np.abs(values), offsets) if operation == "sum" else np.abs(expected)
-    rtol, atol = tolerances[input_dtype]
-    finite = np.isfinite(expected)
-    error = np.abs(actual[finite] - expected[finite])
-    bound = atol + rtol * scale[finite]
-    failures = error > bound
-    if np.any(failures):
-        raise AssertionError(
-            f"{operation}/{input_dtype}: {int(np.sum(failures))} finite values exceed "
-            f"tolerance; max abs error={float(np.max(error)):.9g}")
-    if operation == "softmax":
-        if np.any(actual[finite] < 0) or np.any(actual[finite] > 1):
-            raise AssertionError("finite softmax probabilities must lie in [0, 1]")
-        offsets64 = np.asarray(offsets).astype(np.int64)
-        lengths, mask, starts = _nonempty(offsets64)
-        if starts.size:
-            lo, hi = int(starts[0]), int(offsets64[-1])
-            # Per segment and column: is every expected entry finite, and the
-            # float64 column total of the actual output.
-            valid = np.logical_and.reduceat(finite[lo:hi], starts - lo, axis=0)
-            with np.errstate(invalid="ignore"):
-                totals = np.add.reduceat(np.where(finite, actual, 0.0)[lo:hi], starts - lo, axis=0)
-            if np.any(np.abs(totals[valid] - 1) > rtol + atol):
-                raise AssertionError("finite softmax columns must sum to one within dtype tolerance")
-    return {
-        "finite_values": int(np.sum(finite)),
-        "nan_values": int(np.sum(np.isnan(expected))),
-        "max_abs_error": float(np.max(error, initial=0)),
-        "max_fraction_of_tolerance": float(np.max(error / bound, initial=0)),
-    }
+    return Expectation(values, offsets, operation=operation, input_dtype=input_dtype).check(actual, tolerances)

@@ -126,6 +126,7 @@ struct rg_module {
   uint32_t lds[RG_ROLE_COUNT];
   bool fused;                 // softmax through k_softmax_fused (+ k_softmax_deferred)
   int64_t spin_ticks;         // wall-clock ticks of a chunk's bounded wait
+  int64_t drain_ticks;        // wall-clock ticks of a worker split part's wait for its statistics
   int64_t clock_khz;          // wall-clock rate
   int64_t* trace;             // item timeline buffer (diagnostics) or null
   int64_t trace_cap;
@@ -137,7 +138,7 @@ extern "C" {
 int rg_abi_version(void) { return RG_ABI_VERSION; }
 
 const char* rg_build_info(void) {
-  return "target=gfx950;abi=" "1" ";flags=-O3 -packed-fp32-ops;source=" RG_SOURCE_DIGEST;
+  return "target=gfx950;abi=2;flags=-O3 -packed-fp32-ops;source=" RG_SOURCE_DIGEST;
 }
 
 const char* rg_last_error(void) { return g_error.c_str(); }
@@ -268,6 +269,10 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
   // A chunk waits at most 2 ms for the rest of its segment before deferring.
   module->clock_khz = std::max(clock_khz, 1000);
   module->spin_ticks = module->clock_khz * 2;
+  // A worker's split part waits at most 1 s for its segment's statistics
+  // before it is left to the grid's last workgroup (the wait normally ends
+  // in microseconds).
+  module->drain_ticks = module->clock_khz * 1000;
   for (int role = 0; role < RG_ROLE_COUNT && err == hipSuccess; ++role) {
     module->resident[role] = 0;
     module->lds[role] = 0;
@@ -345,9 +350,15 @@ int rg_profile_stop(rg_module* module, double* role_ms, int64_t* role_launches, 
 }
 
 int rg_module_set_spin_limit(rg_module* module, int64_t microseconds) {
-  if (!module || microseconds < 0 || microseconds > 10000000)
-    return fail(RG_E_INVALID, "rg_module_set_spin_limit: limit must be in [0, 10 s]");
+  if (!module || microseconds < -1 || microseconds > 10000000)
+    return fail(RG_E_INVALID, "rg_module_set_spin_limit: limit must be -1 (defaults) or in [0, 10 s]");
+  if (microseconds < 0) {
+    module->spin_ticks = module->clock_khz * 2;
+    module->drain_ticks = module->clock_khz * 1000;
+    return RG_OK;
+  }
   module->spin_ticks = module->clock_khz * microseconds / 1000;
+  module->drain_ticks = module->spin_ticks;
   return RG_OK;
 }
 
@@ -411,7 +422,6 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     plan->lds_bytes[i] = module->lds[role];
   };
   const int64_t tiles_block = feature_tiles(d, geo.vec, geo.flat, rg::kBlock);
-  const int64_t tiles_wave = feature_tiles(d, geo.vec, geo.flat, rg::kWave);
   if (schedule == RG_BLOCK_PER_SEGMENT) {
     add_launch(RG_ROLE_NAIVE, b, tiles_block);
     return RG_OK;
@@ -450,6 +460,9 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
       sizes[RG_BUF_PARTIAL_SUMS] = item_bytes;
       sizes[RG_BUF_STATS_MAX] = stat_bytes;
       sizes[RG_BUF_STATS_SUM] = stat_bytes;
+      // Split parts (x feature tiles) whose wait for their statistics ran
+      // out, normalised by the worker's last workgroup.
+      if (!mul_ok(items_cap, tiles_block * 8, &sizes[RG_BUF_DEFERRED])) return fail(RG_E_INVALID, "deferred bytes overflow");
     }
   } else {
     // Register-resident softmax: item descriptors, published (m, s) pairs
@@ -495,15 +508,21 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   return RG_OK;
 }
 
-int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets, void* out,
-           const float* mask, void* workspace, uint64_t workspace_bytes, void* stream) {
-  if (!module || !plan) return fail(RG_E_INVALID, "rg_run: null module or plan");
+}  // extern "C"
+
+// Enqueue `plan` with `workspace` (rg_run). `profiled`: the
+// call may record HIP events (rg_profile_start), which creates them; the
+// allocation-free entry point passes false.
+static int enqueue(const char* entry, const rg_module* module, const rg_plan* plan, const void* values,
+                   const void* offsets, void* out, const float* mask, void* workspace, uint64_t workspace_bytes,
+                   void* stream, bool profiled) {
+  if (!module || !plan) return fail(RG_E_INVALID, "%s: null module or plan", entry);
   const rg_spec& spec = module->spec;
   if ((mask != nullptr) != (spec.has_mask != 0)) return fail(RG_E_INVALID, "mask presence must match the module");
   if (plan->launches == 0) return RG_OK;
   // N = 0 leaves values (and a softmax output) empty, possibly null.
   if (!offsets || (plan->n > 0 && (!values || !out)) || (spec.op != RG_OP_SOFTMAX && !out))
-    return fail(RG_E_INVALID, "rg_run: null tensor pointer");
+    return fail(RG_E_INVALID, "%s: null tensor pointer", entry);
   if (plan->workspace_bytes && (!workspace || workspace_bytes < plan->workspace_bytes))
     return fail(RG_E_WORKSPACE, "workspace of %llu bytes is smaller than the plan's %llu",
                 (unsigned long long)workspace_bytes, (unsigned long long)plan->workspace_bytes);
@@ -534,9 +553,7 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
   p.short_segments = plan->schedule == RG_SHORT_SEGMENTS ? 1 : 0;
   p.alone_rows = spec.alone_rows;
   if (plan->schedule == RG_CLASSIFIED) {
-    // A split part's wait for its segment's statistics ends by itself (see
-    // normalize_part); one second bounds it all the same.
-    p.drain_ticks = module->clock_khz * 1000;
+    p.drain_ticks = module->drain_ticks;
     p.counters = static_cast<int64_t*>(buffer(RG_BUF_COUNTERS));
     p.queue = static_cast<int64_t*>(buffer(RG_BUF_QUEUE));
     p.item_pos = static_cast<int64_t*>(buffer(RG_BUF_ITEM_POS));
@@ -566,7 +583,7 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
   if (err != hipSuccess) return hip_fail(err, "hipSetDevice");
   hipStream_t s = static_cast<hipStream_t>(stream);
   Profile& profile = module->profile;
-  const bool record = profile.active && (int)profile.call_first.size() < profile.max_calls;
+  const bool record = profiled && profile.active && (int)profile.call_first.size() < profile.max_calls;
   auto mark = [&]() {
     hipEvent_t event;
     if (err == hipSuccess) err = hipEventCreate(&event);
@@ -597,6 +614,13 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
   if (previous != module->device) (void)hipSetDevice(previous);
   if (err != hipSuccess) return hip_fail(err, "hipLaunchKernel");
   return RG_OK;
+}
+
+extern "C" {
+
+int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets, void* out,
+           const float* mask, void* workspace, uint64_t workspace_bytes, void* stream) {
+  return enqueue("rg_run", module, plan, values, offsets, out, mask, workspace, workspace_bytes, stream, true);
 }
 
 int rg_check_offsets(int device, int offsets_dtype, const void* offsets, int64_t n, int64_t b, int64_t min_len,

@@ -27,6 +27,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace rg {
 
 enum : int { OP_SUM = 0, OP_MAX = 1, OP_SOFTMAX = 2 };
@@ -61,6 +63,46 @@ __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 // IEEE-754 maximum: NaN if either operand is NaN (v_maximum3_f32 on gfx950).
 __device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
+// exp of a softmax output (and of what scales one) for data of type T: f32
+// outputs take the library's accurate expf (about 1 ulp; __expf scales its
+// argument by log2(e) in f32 first, a relative error that grows with
+// |x - m|), bf16 outputs the fast form, far below their rounding.
+template <class T>
+__device__ __forceinline__ float exp_out(float x) {
+  if constexpr (std::is_same<T, float>::value) return expf(x);
+  else return __expf(x);
+}
+// e = exp(x - m) in [0, 1] of bf16 rows held in registers between the two
+// passes of the register-resident softmax, as 16-bit unsigned normalised
+// integers (v_cvt_pknorm_u16_f32, round to nearest): an absolute error of at
+// most 2^-17, far below the bf16 output's own rounding, where storing e as
+// bf16 would round twice. NaN stores as 0; a NaN e only occurs in columns
+// whose scale factor is NaN, so the output stays NaN.
+constexpr float kUnormScale = 1.0f / 65535.0f;
+__device__ __forceinline__ uint32_t pack_unorm(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_u16(lo, hi));
+}
+__device__ __forceinline__ float unorm_lo(uint32_t w) { return (float)(w & 0xffffu); }
+__device__ __forceinline__ float unorm_hi(uint32_t w) { return (float)(w >> 16); }
+
+// Workgroup-wide OR of `x` for the kBlock-thread workgroups of every kernel
+// here: one ballot per wave, one LDS flag per wave, two barriers. HIP's
+// __syncthreads_or reads the workgroup size from the dispatch packet first
+// (three 16-bit global loads and a wait for them), a full memory round trip
+// per call that lands on the critical path of every poll of a waiting chunk.
+// Every thread of the workgroup must call it (it contains barriers).
+__device__ __forceinline__ bool block_any(bool x) {
+  __shared__ int any_s[kWavesPerBlock];
+  const bool wave_any = __ballot(x) != 0;
+  if ((threadIdx.x & (kWave - 1)) == 0) any_s[threadIdx.x / kWave] = wave_any ? 1 : 0;
+  __syncthreads();
+  int any = 0;
+#pragma unroll
+  for (int w = 0; w < kWavesPerBlock; ++w) any |= any_s[w];
+  // No wave may overwrite its flag (next call) before every wave has read it.
+  __syncthreads();
+  return any != 0;
+}
 
 // One work item of the register-resident softmax: a whole segment (k < 0)
 // or chunk c of `parts` of a long segment at split-queue position k.
@@ -89,13 +131,15 @@ struct Params {
   int64_t part_rows;       // rows per split part
   int64_t items_cap;       // capacity of the split item tables
   int64_t b_split;         // capacity of the split queue / statistics rows
-  int64_t* counters;       // slots 0-10: wave (reduced alone), block, split segment
+  int64_t* counters;       // slots 0-11: wave (reduced alone), block, split segment
                            //      counts; split items; work ticket; deferred
-                           //      chunks; tree items; the wave count of a
-                           //      register-resident softmax; the rest of the wave
-                           //      class; the split-part normalisation ticket;
-                           //      normalisation waits past their bound. Then the
-                           //      worker's ticket lanes (kTicketStride apart)
+                           //      chunks (register-resident softmax) or split
+                           //      parts (worker softmax); tree items; the wave
+                           //      count of a register-resident softmax; the rest
+                           //      of the wave class; the split-part normalisation
+                           //      ticket; unused; workgroups finished (worker
+                           //      softmax). Then the worker's ticket lanes
+                           //      (kTicketStride apart)
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item
   int64_t* part_begin;     // [B] first item of each split-queue position
@@ -104,7 +148,9 @@ struct Params {
   float* stats_max;        // [B_split, D] combined softmax reference
   float* stats_sum;        // [B_split, D] combined softmax mass
   int32_t* visits;         // [B] or null (debug)
-  int64_t* deferred;       // [items_cap] chunks left to the re-read pass
+  int64_t* deferred;       // [items_cap] chunks left to the re-read pass (register-resident
+                           // softmax); [items_cap * tiles] split parts left to the last
+                           // workgroup (worker softmax)
   int32_t* arrive;         // [items_cap] chunk arrivals per 32-chunk group (slot: group's first item)
   int32_t* seg_arrive;     // [B_split] group arrivals per split segment
   Item* items;             // [items_cap] split chunks (register-resident softmax)

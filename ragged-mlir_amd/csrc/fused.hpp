@@ -59,6 +59,7 @@ constexpr int kOutOfRange = 0x7ff00000;  // byte offset beyond any chunk resourc
 // the loads go through the scalar cache into SGPRs (no VGPRs held while a
 // prefetch is in flight).
 typedef __attribute__((address_space(4))) const Item ConstItem;
+typedef __attribute__((address_space(4))) const int64_t ConstI64;
 
 __device__ __forceinline__ Item load_item(ConstItem* item) {
   Item it;
@@ -280,7 +281,7 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
       lds_m[f] = st.m;
       lds_s[f] = st.s;
     }
-    return __syncthreads_or(!ok) == 0;
+    return !block_any(!ok);
   }
   if (t < r * d) {
     const int part = t / d, f = t - part * d;
@@ -288,7 +289,7 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
     const State<OP_SOFTMAX> st = fold_range(base + lo * stride * d, hi - lo, stride, d, f, ok);
     stage[t] = pack_pair(st.m, st.s);
   }
-  const bool all = __syncthreads_or(!ok) == 0;
+  const bool all = !block_any(!ok);
   if (all && t < d) {
     State<OP_SOFTMAX> acc;
     acc.init();
@@ -312,7 +313,7 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
   const long long start = wall_clock64();
   for (;;) {
     if (fold_block(base, count, 1, d, lds_m, lds_s, stage)) return true;
-    if (__syncthreads_or(threadIdx.x == 0 && wall_clock64() - start >= spin_ticks)) return false;
+    if (block_any(threadIdx.x == 0 && wall_clock64() - start >= spin_ticks)) return false;
     __builtin_amdgcn_s_sleep(kPollSleep);
   }
 }
@@ -320,7 +321,10 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
 // Counter-based tree merge of a long segment: the last chunk of each group
 // folds the group into slot gfirst (into final_pairs[k] when the segment is
 // one group), the last group folds the groups into final_pairs[k]. Never
-// waits.
+// waits: every slot a fold reads was published (stores complete, then the
+// barrier) before the counter increment that made this workgroup the last.
+// The group fold replaces chunk gfirst's own pair, so a deferred chunk takes
+// its own column max from its rows, not from its pair slot.
 __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t k, int* flag_s,
                            float* lds_m, float* lds_s, uint64_t* stage) {
   const int t = threadIdx.x;
@@ -359,6 +363,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   using Store = typename std::conditional<STORE_F32, float, T>::type;
   using In = Words<T, VEC>;
   using Reg = Words<Store, VEC>;
+  // Pass 1 replaces each row by e = exp(x - m) and pass 2 writes e times the
+  // column's factor exp(m - M) / S. f32 rows (f32 data, or the f32 logits a
+  // scale or mask makes of bf16 data) keep e in f32; bf16 rows keep it as a
+  // 16-bit unorm (pack_unorm), whose 1/65535 the factor carries, so the
+  // output is rounded to bf16 once.
+  constexpr bool kUnorm = !STORE_F32 && !std::is_same<T, float>::value;
   // lds: reductions, then the segment's merged max per feature; lds_s: its sum.
   __shared__ float lds[kBlock * VEC];
   __shared__ float lds_s[kBlock * VEC];
@@ -389,11 +399,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   // of counters[0] -- k_softmax_deferred takes it after this kernel -- so
   // the last term is 0. It stays: without it the compiler allocates this
   // kernel's scalar registers differently and it runs slower.
-  const int64_t n_tree = p.counters[6] < p.items_cap ? p.counters[6] : p.items_cap;
-  const int64_t n_direct = p.counters[3] < p.items_cap - n_tree ? p.counters[3] : p.items_cap - n_tree;
+  // The class counts were written by k_classify and stay fixed during this
+  // kernel: read through the constant address space they load into SGPRs
+  // (scalar loads) instead of occupying vector registers, which the held
+  // rows need.
+  const ConstI64* counts = (const ConstI64*)p.counters;
+  const int64_t n_tree = counts[6] < p.items_cap ? counts[6] : p.items_cap;
+  const int64_t n_direct = counts[3] < p.items_cap - n_tree ? counts[3] : p.items_cap - n_tree;
   const int64_t n_split = n_tree + n_direct;
-  const int64_t n_block = p.counters[1];
-  const int64_t total = n_split + n_block + p.counters[0];
+  const int64_t n_block = counts[1];
+  const int64_t total = n_split + n_block + counts[0];
   const int64_t d = p.d;
   // Byte offsets inside an item: per thread, and the stride between a
   // thread's rows.
@@ -517,10 +532,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       float e[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        e[v] = fast_exp(Reg::get(data[i], v) - ref[v]);
+        e[v] = exp_out<T>(Reg::get(data[i], v) - ref[v]);
         sum[v] += e[v];
       }
-      Reg::set(data[i], e);
+      if constexpr (kUnorm) {
+        if constexpr (VEC == 1) {
+          data[i][0] = pack_unorm(e[0], 0.f) & 0xffffu;
+        } else {
+#pragma unroll
+          for (int w = 0; w < Reg::kCount; ++w) data[i][w] = pack_unorm(e[2 * w], e[2 * w + 1]);
+        }
+      } else {
+        Reg::set(data[i], e);
+      }
       // Pack now, so that the f32 values die here rather than after the
       // reduction below.
 #pragma unroll
@@ -538,10 +562,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       }
     }
     __syncthreads();
-    // 3. Scale factor per column, into lds[f]: exp(m - M) / S.
+    // 3. Scale factor per column, into lds[f]: exp(m - M) / S (times
+    //    1/65535 for unorm rows).
+    const float unit = kUnorm ? kUnormScale : 1.0f;
     bool defer = false;
     if (!chunk) {
-      for (int f = t; f < d; f += kBlock) lds[f] = fast_exp(own_m[f] - own_m[f]) / own_s[f];
+      for (int f = t; f < d; f += kBlock) lds[f] = exp_out<T>(own_m[f] - own_m[f]) / own_s[f] * unit;
     } else {
       const int64_t idx = index_of(ticket);
       const int64_t first = idx - it.c;
@@ -557,7 +583,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         defer = !ready;
         // Same thread wrote lds[f] / lds_s[f] in the fold: no barrier needed.
         if (ready) {
-          for (int f = t; f < d; f += kBlock) lds[f] = fast_exp(own_m[f] - lds[f]) / lds_s[f];
+          for (int f = t; f < d; f += kBlock) lds[f] = exp_out<T>(own_m[f] - lds[f]) / lds_s[f] * unit;
         }
       }
       if (t == 0 && defer) {
@@ -581,7 +607,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         if (!live(i)) continue;
         float y[VEC];
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) y[v] = Reg::get(data[i], v) * factor[v];
+        for (int v = 0; v < VEC; ++v) {
+          const float e = kUnorm ? ((v & 1) ? unorm_hi(data[i][v >> 1]) : unorm_lo(data[i][v >> 1]))
+                                 : Reg::get(data[i], v);
+          y[v] = e * factor[v];
+        }
         uint32_t w[In::kCount];
         In::set(w, y);
         buffer_store<In::kBytes>(out, voff + i * step_in, 0, w);
@@ -610,34 +640,71 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   }
 }
 
+// Rows [r0, r1) of a deferred chunk with the arithmetic k_softmax_fused
+// would have used in registers, so a chunk's bits do not depend on whether
+// it waited: e = exp(x - ref) with the chunk's own reference, as a 16-bit
+// unorm for bf16 rows held as loaded (`unorm`), times the chunk's factor.
+template <class T, int VEC, bool MASK>
+__device__ __forceinline__ void renormalize_rows(const Params& p, const RowGeo& g, int64_t r0, int64_t r1, bool unorm,
+                                                 const float (&ref)[VEC], const float (&factor)[VEC]) {
+  if (!g.active) return;
+  T* out = static_cast<T*>(p.out);
+  for (int64_t r = r0 + g.row_lane; r < r1; r += g.rows_step) {
+    float x[VEC];
+    load_input<T, VEC, MASK>(p, r * p.d + g.feature, x);
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+      float e = exp_out<T>(x[v] - ref[v]);
+      if (unorm) e = unorm_lo(pack_unorm(e, 0.f));
+      x[v] = e * factor[v];
+    }
+    Elem<T>::template store<VEC>(out + r * p.d + g.feature, x);
+  }
+}
+
 // Chunks that did not normalise in k_softmax_fused (spin limit, or a segment
 // longer than the device holds at once): re-read and normalise with the
-// segment's merged statistics, complete once k_softmax_fused has finished.
-// Then the wave class, which k_softmax_fused does not take (k_classify
-// counts it in counters[7]), in the streaming worker's batches: a ticket per
-// short segment would serialise k_softmax_fused on its ticket counter.
+// segment's merged statistics, complete once k_softmax_fused has finished,
+// and the chunk's own column max, by the register path's arithmetic
+// (renormalize_rows). Then the wave class, which k_softmax_fused
+// does not take (k_classify counts it in counters[7]), in the streaming
+// worker's batches: a ticket per short segment would serialise
+// k_softmax_fused on its ticket counter.
 template <class T, class OffT, int VEC, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
   const int64_t count = p.counters[5] < p.items_cap ? p.counters[5] : p.items_cap;
   const int t = threadIdx.x;
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
+  // The register-resident kernel that ran held bf16 rows as loaded (e as
+  // unorm) unless a scale or mask made f32 logits of them (its STORE_F32
+  // variant, e in f32).
+  const bool unorm = !MASK && !std::is_same<T, float>::value && !p.has_scale;
+  const float unit = unorm ? kUnormScale : 1.0f;
   __shared__ float lds_m[kBlock * VEC], lds_s[kBlock * VEC];
   __shared__ uint64_t stage[kBlock];
   for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
     const int64_t slot = p.deferred[i];
     const Item it = p.items[slot];
+    // The chunk's own column max, from its rows (the tree merge may have
+    // replaced its published pair by its group's): IEEE maximum is exact in
+    // any order, so it equals the register path's.
+    State<OP_MAX> own[VEC];
+    init_all<OP_MAX, VEC>(own);
+    fold_rows<OP_MAX, T, VEC, MASK>(p, g, it.start, it.start + it.rows, own);
+    block_reduce<OP_MAX, VEC>(own, g.lpr, g.feat_lane, lds_m);
     // Every pair is published once k_softmax_fused has finished.
     if (it.parts <= kDirect) (void)fold_block(p.pairs + (slot - it.c) * p.d, it.parts, 1, p.d, lds_m, lds_s, stage);
     else (void)fold_block(p.final_pairs + it.k * p.d, 1, 1, p.d, lds_m, lds_s, stage);
     __syncthreads();
     if (g.active) {
-      float m[VEC], inv[VEC];
+      float ref[VEC], factor[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        m[v] = lds_m[g.feature + v];
-        inv[v] = 1.0f / lds_s[g.feature + v];
+        const int f = g.feature + v;
+        ref[v] = own[v].m == neg_inf() ? 0.f : own[v].m;
+        factor[v] = exp_out<T>(own[v].m - lds_m[f]) / lds_s[f] * unit;
       }
-      normalize_rows<T, VEC, MASK>(p, g, it.start, it.start + it.rows, m, inv);
+      renormalize_rows<T, VEC, MASK>(p, g, it.start, it.start + it.rows, unorm, ref, factor);
     }
     if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     __syncthreads();

@@ -100,7 +100,7 @@ __device__ __forceinline__ void normalize_rows(const Params& p, const RowGeo& g,
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) x[u][v] = fast_exp(x[u][v] - m[v]) * inv[v];
+      for (int v = 0; v < VEC; ++v) x[u][v] = exp_out<T>(x[u][v] - m[v]) * inv[v];
       Elem<T>::template store<VEC>(out + (r + u * step) * d + g.feature, x[u]);
     }
   }
@@ -108,7 +108,7 @@ __device__ __forceinline__ void normalize_rows(const Params& p, const RowGeo& g,
     float x[VEC];
     load_input<T, VEC, MASK>(p, r * d + g.feature, x);
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) x[v] = fast_exp(x[v] - m[v]) * inv[v];
+    for (int v = 0; v < VEC; ++v) x[v] = exp_out<T>(x[v] - m[v]) * inv[v];
     Elem<T>::template store<VEC>(out + r * d + g.feature, x);
   }
 }
@@ -184,14 +184,14 @@ __device__ __forceinline__ void normalize_flat(const Params& p, int g, int t, in
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int64_t e = j * VEC + c;
-      if (e >= lo && e < hi) Elem<T>::put(out + e, fast_exp(x[c] - m[c]) * inv[c]);
+      if (e >= lo && e < hi) Elem<T>::put(out + e, exp_out<T>(x[c] - m[c]) * inv[c]);
     }
   }
   for (int64_t j = full_lo + t; j < full_hi; j += g) {
     float x[VEC];
     load_input<T, VEC, MASK>(p, j * VEC, x);
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) x[c] = fast_exp(x[c] - m[c]) * inv[c];
+    for (int c = 0; c < VEC; ++c) x[c] = exp_out<T>(x[c] - m[c]) * inv[c];
     Elem<T>::template store<VEC>(out + j * VEC, x);
   }
 }

@@ -161,7 +161,7 @@ __device__ __forceinline__ void lane_softmax_held(const Params& p, int64_t lo, i
   for (int u = 0; u < K; ++u) {
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
-      x[u][c] = fast_exp(x[u][c] - ref[c]);
+      x[u][c] = exp_out<T>(x[u][c] - ref[c]);
       s[c] += inside(u, c) ? x[u][c] : 0.f;
     }
   }
@@ -225,7 +225,7 @@ __device__ __forceinline__ void lane_softmax(const Params& p, int64_t lo, int64_
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int64_t e = j * VEC + c;
-      if (e >= lo && e < hi) s[c] += fast_exp(x[c] - ref[c]);
+      if (e >= lo && e < hi) s[c] += exp_out<T>(x[c] - ref[c]);
     }
   });
   fold_residues<false, VEC>(s, d);
@@ -236,7 +236,7 @@ __device__ __forceinline__ void lane_softmax(const Params& p, int64_t lo, int64_
   pass([&](int64_t j, const float (&in)[VEC]) {
     float x[VEC];
 #pragma unroll
-    for (int c = 0; c < VEC; ++c) x[c] = fast_exp(in[c] - ref[c]) * inv[c];
+    for (int c = 0; c < VEC; ++c) x[c] = exp_out<T>(in[c] - ref[c]) * inv[c];
     if (j * VEC >= lo && j * VEC + VEC <= hi) {
       Elem<T>::template store<VEC>(out + j * VEC, x);   // a whole vector of this segment
     } else {
@@ -306,7 +306,7 @@ __device__ __forceinline__ void group_segment(const Params& p, int64_t s, int64_
       for (int v = 0; v < VEC; ++v) ref[v] = m[v] == neg_inf() ? 0.f : m[v];
       rows([&](int64_t, const float (&x)[VEC]) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) sum[v] += fast_exp(x[v] - ref[v]);
+        for (int v = 0; v < VEC; ++v) sum[v] += exp_out<T>(x[v] - ref[v]);
       });
 #pragma unroll
       for (int v = 0; v < VEC; ++v) inv[v] = fast_exp(m[v] - m[v]) / sum[v];   // NaN for an all -inf column
@@ -314,7 +314,7 @@ __device__ __forceinline__ void group_segment(const Params& p, int64_t s, int64_
       rows([&](int64_t r, const float (&x)[VEC]) {
         float y[VEC];
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) y[v] = fast_exp(x[v] - ref[v]) * inv[v];
+        for (int v = 0; v < VEC; ++v) y[v] = exp_out<T>(x[v] - ref[v]) * inv[v];
         Elem<T>::template store<VEC>(out + r * d + f0, y);
       });
     } else {
@@ -371,22 +371,25 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
     }
   }
   // Arrival: once this part's stores have completed (every thread waits
-  // for its own, then the barrier), count it at the segment.
+  // for its own, then the barrier), count it at the segment. The segment's
+  // parts are the items [first, stop) that exist: valid offsets always give
+  // all of them; offsets that break the contract can reserve items past
+  // items_cap, which are never run, so the target counts only those below.
   int64_t seg_start, seg_end;
   segment_rows<OffT>(p, s, seg_start, seg_end);
   const int64_t all_parts = (seg_end - seg_start + p.part_rows - 1) / p.part_rows;
   const int tiles = FLAT ? 1 : tiles_of<VEC>(p.d, kBlock);
+  const int64_t first = p.part_begin[k];
+  const int64_t stop = first + all_parts < p.items_cap ? first + all_parts : p.items_cap;
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
-  if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == all_parts * tiles - 1;
+  if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == (stop - first) * tiles - 1;
   __syncthreads();
   const bool last = *flag_s != 0;
   __syncthreads();
   if (!last) return;
   // Combine: threads = part lanes x features, LDS tree over part lanes, the
   // parts folded in order within each lane and lanes in order.
-  const int64_t first = p.part_begin[k];
-  const int64_t stop = first + all_parts < p.items_cap ? first + all_parts : p.items_cap;
   const int ft = combine_features(p.d);
   const int pl_count = kBlock / ft;
   const int fl = t % ft, pl = t / ft;
@@ -435,26 +438,31 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
 
 // Softmax probabilities of split part `item` (feature tile `tile`) with its
 // segment's combined statistics (ToGPU.cpp:279-281), once the segment's last
-// part has published them. The wait ends: every part was handed to a running
-// workgroup before any workgroup gets here, and a part never waits. A
-// wall-clock bound (drain_ticks) guards against a hang all the same; running
-// out of it is counted in counters[10].
+// part has published them. With `wait`, the workgroup waits for them for at
+// most drain_ticks and returns false, having written nothing, if they are
+// still out: the caller defers the part (k_worker). The wait normally ends
+// well before: every part was handed to a running workgroup before any
+// workgroup gets here, and a part never waits. Without `wait` the statistics
+// must already be published.
 template <class T, class OffT, int VEC, bool FLAT, bool MASK>
-__device__ __forceinline__ void normalize_part(const Params& p, int64_t item, int tile) {
+__device__ __forceinline__ bool normalize_part(const Params& p, int64_t item, int tile, bool wait) {
   const int t = threadIdx.x;
   int64_t k, s, part, start, end;
   item_rows<OffT>(p, item, k, s, part, start, end);
-  if (t == 0) {
-    const long long t0 = wall_clock64();
-    while (__hip_atomic_load(p.seg_arrive + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != kStatsReady) {
-      if (wall_clock64() - t0 >= p.drain_ticks) {
-        atomicAdd((unsigned long long*)(p.counters + 10), 1ull);
-        break;
+  if (wait) {
+    bool ready = true;
+    if (t == 0) {
+      const long long t0 = wall_clock64();
+      while (__hip_atomic_load(p.seg_arrive + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != kStatsReady) {
+        if (wall_clock64() - t0 >= p.drain_ticks) {
+          ready = false;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
-      __builtin_amdgcn_s_sleep(2);
     }
+    if (block_any(!ready)) return false;
   }
-  __syncthreads();
   float m[VEC], inv[VEC];
   if constexpr (FLAT) {
 #pragma unroll
@@ -476,6 +484,7 @@ __device__ __forceinline__ void normalize_part(const Params& p, int64_t item, in
     }
   }
   if (p.visits && part == 0 && tile == 0 && t == 0) atomicAdd(p.visits + s, 1);
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -598,7 +607,10 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   }
   // Softmax: the split parts' probabilities, from a counter of their own,
   // once this workgroup's tickets have run out (so every part has been
-  // handed out).
+  // handed out). A part whose statistics are not out within drain_ticks is
+  // deferred (counters[5] entries of `deferred`, agent scope); the last
+  // workgroup to finish (counters[11]) normalises those: by then every part
+  // has run and every segment's statistics are published.
   if constexpr (OP == OP_SOFTMAX) {
     if (n_parts > 0) {
       for (;;) {
@@ -609,7 +621,24 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
                                      << 32) |
                                     __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)ticket_s));
         if (i >= n_parts) break;
-        normalize_part<T, OffT, VEC, FLAT, MASK>(p, i / tiles_block, (int)(i % tiles_block));
+        if (!normalize_part<T, OffT, VEC, FLAT, MASK>(p, i / tiles_block, (int)(i % tiles_block), true) && t == 0) {
+          const int64_t slot = (int64_t)atomicAdd((unsigned long long*)(p.counters + 5), 1ull);
+          if (slot < n_parts) __hip_atomic_store(p.deferred + slot, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      // Every store of this workgroup (deferred entries, statistics of the
+      // segments it combined) completes before it counts itself finished.
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      __syncthreads();
+      if (t == 0) flag_s = atomicAdd((unsigned long long*)(p.counters + 11), 1ull) == gridDim.x - 1;
+      __syncthreads();
+      if (flag_s) {
+        const int64_t deferred = __hip_atomic_load(p.counters + 5, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t count = deferred < n_parts ? deferred : n_parts;
+        for (int64_t j = 0; j < count; ++j) {
+          const int64_t i = __hip_atomic_load(p.deferred + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          (void)normalize_part<T, OffT, VEC, FLAT, MASK>(p, i / tiles_block, (int)(i % tiles_block), false);
+        }
       }
     }
   }

@@ -217,7 +217,10 @@ class NativeModule:
             _check(status, "rg_run")
 
     def set_spin_limit(self, microseconds: int) -> None:
-        """Bound of a softmax chunk's wait for its segment (test control)."""
+        """Bound of every softmax wait for other workgroups' statistics: a
+        register-resident chunk's wait for its segment and a worker split
+        part's wait for its segment's statistics (test control; -1 restores
+        the defaults)."""
         _check(library().rg_module_set_spin_limit(self._handle, microseconds), "rg_module_set_spin_limit")
 
     def set_trace(self, buffer: int | None, records: int = 0) -> None:

@@ -5,7 +5,12 @@ the generator arguments and the sha256 of the generated lengths, offsets and
 values (``bench/run.py:51-65`` -> ``results/**/results.json`` "case" and
 "command"). Those records are data; this script copies the fields needed to
 pin ``ragged.workloads`` (the restated generators) into a small fixture. It
-reads JSON only and runs no reference code.
+also copies, for the comparison runs of seed 711
+(``results/bench/runs/compare/*/seed-711/rep-0``), the oracle statistics the
+reference recorded for every measured method (``methods[].oracle``:
+max_abs_error, max_fraction_of_tolerance), so the GPU tests can regenerate
+those inputs and compare this build's error with the reference's. It reads
+JSON only and runs no reference code.
 
 Usage: python tests/golden/make_reference_cases.py [/root/reference]
 """
@@ -20,6 +25,32 @@ def _argument(command: list[str], flag: str, default=None):
     if flag in command:
         return command[command.index(flag) + 1]
     return default
+
+
+def recorded_oracle(reference: Path) -> list[dict]:
+    """Per comparison case (seed 711, first repetition): the op and generator
+    arguments, and each measured method's recorded oracle statistics."""
+    records = []
+    for path in sorted((reference / "results" / "bench" / "runs" / "compare").glob("*/seed-711/rep-0/results.json")):
+        record = json.loads(path.read_text())
+        case, command = record["case"], record["command"]
+        methods = {}
+        for method in record["methods"]:
+            stats = method.get("oracle")
+            if method.get("status", "measured") == "measured" and isinstance(stats, dict):
+                methods[method["method"]] = {key: stats[key] for key in
+                                             ("max_abs_error", "max_fraction_of_tolerance", "finite_values",
+                                              "nan_values")}
+        total = _argument(command, "--total-elements")
+        records.append({
+            "op": case["op"], "distribution": case["distribution"], "segments": int(case["segments"]),
+            "total_elements": int(total) if total is not None else None,
+            "mean_length": int(_argument(command, "--mean-length", 64)), "seed": int(case["seed"]),
+            "d": int(case["D"]), "dtype": case["dtype"], "offsets_dtype": case["offsets_dtype"],
+            "lengths_sha256": case["lengths_sha256"], "values_sha256": case["values_sha256"],
+            "methods": methods, "source": str(path.relative_to(reference)),
+        })
+    return records
 
 
 def main(reference: Path) -> int:
@@ -56,9 +87,12 @@ def main(reference: Path) -> int:
     # Keep every distinct generator case whose values are cheap to regenerate.
     chosen = sorted(cases.values(), key=lambda e: (e["elements"] * e["d"], e["source"]))
     small = [e for e in chosen if e["elements"] * e["d"] <= 2**25]
+    recorded = recorded_oracle(reference)
     out = Path(__file__).with_name("reference_cases.json")
-    out.write_text(json.dumps({"cases": small, "total_distinct": len(chosen)}, indent=1) + "\n")
-    print(f"wrote {len(small)} of {len(chosen)} distinct cases to {out}")
+    out.write_text(json.dumps({"cases": small, "total_distinct": len(chosen), "recorded_oracle": recorded},
+                              indent=1) + "\n")
+    print(f"wrote {len(small)} of {len(chosen)} distinct cases and {len(recorded)} recorded oracle "
+          f"statistics to {out}")
     return 0
 
 

@@ -46,6 +46,22 @@ def run_program(program, values: np.ndarray, offsets: np.ndarray, *, dtype: str,
     return out.float().cpu().numpy().astype(np.float64), report
 
 
+def check_expectation(actual: np.ndarray, expectation: "oracle.Expectation") -> dict:
+    """``check`` against a precomputed oracle reference (one float64
+    reference for several outputs of the same input): the reference's
+    tolerance, the build's stricter one, and max bit for bit."""
+    stats = expectation.check(actual)
+    expectation.check(actual, oracle.STRICT_TOLERANCES)
+    if expectation.operation == "max":
+        expected = expectation.expected.astype(np.float32)
+        if expectation.input_dtype == "bf16":
+            expected = oracle.quantize_bf16(expected)
+        nan = np.isnan(expected)
+        assert np.array_equal(nan, np.isnan(actual)), "max NaN mask differs"
+        assert np.array_equal(actual[~nan], expected[~nan].astype(np.float64)), "max is not bit-exact"
+    return stats
+
+
 def check(actual: np.ndarray, values: np.ndarray, offsets: np.ndarray, *, op: str, dtype: str,
           mask: np.ndarray | None = None, scale: float = 1.0) -> dict:
     """Oracle contract, plus bit-exactness for max (max selects an input)."""

@@ -1,0 +1,181 @@
+"""GPU contract tests: classification queue order, HIP-graph replay and the
+reference's recorded error statistics.
+
+* Ordered queue runs: k_classify reserves one run of queue positions per
+  class and workgroup, so a workgroup's segments of one class sit in
+  consecutive positions in segment order (the wave64/workgroup restatement
+  of the reference's test/gpu/test_classified.py:161-194 and
+  docs/classified-abi.md:62-73; the reference aggregates per 32-lane warp).
+* Graph replay: a captured ``program.run`` replays bit for bit like an eager
+  call on new inputs, with eager work between the replays (reference
+  test/gpu/test_scheduling.py:151-172).
+* Recorded statistics: the reference's comparison runs (seed 711) recorded
+  each method's oracle error; the same inputs, regenerated, run here within
+  the envelope of the reference's methods (max exactly).
+"""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from gpu_helpers import check, quantized, run_program
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+if not torch.cuda.is_available():  # pragma: no cover - CPU containers
+    pytest.skip("no ROCm device", allow_module_level=True)
+
+from ragged import Compiler, ProgramSpec, native  # noqa: E402
+from ragged.workloads import make_lengths, offsets_from_lengths, reference_values, sha256  # noqa: E402
+
+DEVICE = torch.device("cuda", 0)
+GOLDEN = Path(__file__).resolve().parent / "golden" / "reference_cases.json"
+CLASSIFY_BLOCK, CLASSIFY_LARGE_BLOCK, CLASSIFY_LARGE = 256, 1024, 16384
+
+
+def buffer(workspace, plan, name, dtype):
+    for buf_name, offset, nbytes in plan.buffers:
+        if buf_name == name:
+            return workspace[offset:offset + nbytes].view(dtype)
+    raise KeyError(name)
+
+
+@pytest.mark.parametrize("segments", [1, 63, 64, 65, 255, 256, 257, 1000, 4133, 20000])
+@pytest.mark.parametrize("pattern", ["mixed", "one_class", "rotating"])
+def test_each_workgroup_reserves_one_ordered_run_per_class(segments, pattern):
+    """Thresholds t_wave=64, t_block=4096 with D=2 f32 (16-byte flat
+    mapping, alone_rows 32): run 0 holds the wave-class segments of at most
+    32 rows from the front of queue row 0, run 3 the rest of the wave class
+    from its back, then the block and split rows. Counts and membership
+    match the closed form; within each classify workgroup's window of
+    segments every class's positions are consecutive and increasing."""
+    rng = np.random.default_rng(segments)
+    if pattern == "mixed":
+        lengths = rng.choice([0, 1, 32, 33, 64, 65, 4096, 4097], size=segments)
+    elif pattern == "one_class":
+        lengths = np.full(segments, 40)
+    else:
+        lengths = np.array([0, 100, 5000])[np.arange(segments) % 3]
+    lengths = lengths.astype(np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.integers(-2, 3, size=(int(offsets[-1]), 2)).astype(np.float32)
+    spec = native.make_spec("sum", "f32", "i64", 2, t_wave=64, t_block=4096, part_rows=1024)
+    assert (spec.alone_rows, spec.t_wave, spec.t_block) == (32, 64, 4096)
+    module = native.NativeModule(0, spec)
+    n, b = int(offsets[-1]), segments
+    plan = module.plan(n, b, "classified")
+    x = torch.from_numpy(values).to(DEVICE)
+    off = torch.from_numpy(offsets).to(DEVICE)
+    out = torch.full((b, 2), float("nan"), device=DEVICE)
+    workspace = torch.full((int(plan.workspace_bytes),), 0xEE, dtype=torch.uint8, device=DEVICE)
+    module.run(plan, x.data_ptr(), off.data_ptr(), out.data_ptr(), None, workspace.data_ptr(),
+               int(plan.workspace_bytes), torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    check(out.cpu().numpy().astype(np.float64), values, offsets, op="sum", dtype="f32")
+    counters = buffer(workspace, plan, "class_counts", torch.int64).cpu().numpy()
+    queue = buffer(workspace, plan, "segment_ids", torch.int64).view(3, b).cpu().numpy()
+    run_of = np.where(lengths <= 32, 0, np.where(lengths <= 64, 3, np.where(lengths <= 4096, 1, 2)))
+    counts = {0: int(counters[0]), 3: int(counters[8]), 1: int(counters[1]), 2: int(counters[2])}
+    for run, count in counts.items():
+        assert count == int((run_of == run).sum()), f"run {run}"
+    members = {0: queue[0, :counts[0]], 3: queue[0, b - 1 - np.arange(counts[3])],
+               1: queue[1, :counts[1]], 2: queue[2, :counts[2]]}
+    position = np.full(b, -1, dtype=np.int64)
+    for run, ids in members.items():
+        np.testing.assert_array_equal(np.sort(ids), np.flatnonzero(run_of == run))
+        position[ids] = np.arange(len(ids))
+    window = CLASSIFY_LARGE_BLOCK if b >= CLASSIFY_LARGE else CLASSIFY_BLOCK
+    for first in range(0, b, window):
+        for run in (0, 1, 2, 3):
+            mine = position[first:first + window][run_of[first:first + window] == run]
+            if len(mine):
+                np.testing.assert_array_equal(mine, np.arange(mine[0], mine[0] + len(mine)))
+    module.close()
+
+
+GRAPH_CASES = [
+    # (op, dtype, d, offsets dtype, length distribution, rows): the
+    # register-resident softmax with chunked segments, the classified worker
+    # for a flat reduction and a flat softmax with split parts.
+    ("softmax", "bf16", 128, "i64", "long_tail", 120_000),
+    ("sum", "f32", 1, "i64", "long_tail", 600_000),
+    ("softmax", "f32", 2, "i32", "burst", 400_000),
+]
+
+
+@pytest.mark.parametrize("op,dtype,d,offsets_dtype,distribution,rows", GRAPH_CASES)
+def test_graph_replay_matches_eager_bit_for_bit(artifact_cache, op, dtype, d, offsets_dtype, distribution, rows):
+    program = Compiler().compile(ProgramSpec(op, dtype, d, offsets_dtype), artifact_cache)
+    lengths = make_lengths(distribution, 600, seed=17, total_elements=rows)
+    offsets = offsets_from_lengths(lengths, offsets_dtype)
+    tdtype = torch.bfloat16 if dtype == "bf16" else torch.float32
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.normal(size=(rows, d)).astype(np.float32)).to(DEVICE).to(tdtype)
+    off = torch.from_numpy(offsets).to(DEVICE)
+    out_rows = rows if op == "softmax" else len(lengths)
+    out = torch.empty((out_rows, d), dtype=tdtype, device=DEVICE)
+    eager = torch.empty_like(out)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        program.run(x, off, out, stream=stream, select="classified")   # plan and workspace of this stream
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        report = program.run(x, off, out, stream=stream, select="classified")
+    assert report.selected == "classified" and len(report.kernel_names) >= 3
+    for replay in range(4):
+        values = np.random.default_rng(100 + replay).normal(size=(rows, d)).astype(np.float32) * (1 + replay)
+        x.copy_(torch.from_numpy(values).to(DEVICE).to(tdtype))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        program.run(x, off, eager, select="classified")
+        torch.cuda.synchronize()
+        view = torch.int16 if tdtype == torch.bfloat16 else torch.int32
+        assert torch.equal(out.view(view), eager.view(view)), f"replay {replay} differs from the eager call"
+        check(out.float().cpu().numpy().astype(np.float64), x.float().cpu().numpy(), offsets, op=op, dtype=dtype)
+
+
+def recorded_cases():
+    return json.loads(GOLDEN.read_text())["recorded_oracle"]
+
+
+@pytest.mark.parametrize("case", recorded_cases(), ids=lambda c: f"{c['op']}-{c['dtype']}-d{c['d']}-{c['distribution']}")
+def test_reference_recorded_error_statistics(artifact_cache, case):
+    """The reference recorded, for these exact inputs, every method's oracle
+    error (results/bench/runs/compare/*/seed-711/rep-0/results.json).
+    Max must be exact as there; sum and softmax must stay within 1.5x the
+    worst of the reference's measured methods, and bf16 softmax (whose error
+    is the output's one rounding) within 1.05x the reference's own."""
+    lengths = make_lengths(case["distribution"], case["segments"], seed=case["seed"],
+                           total_elements=case["total_elements"], mean_length=case["mean_length"])
+    offsets = offsets_from_lengths(lengths, case["offsets_dtype"])
+    values = reference_values(case["seed"], int(offsets[-1]), case["d"])
+    op, dtype = case["op"], case["dtype"]
+    # The reference hashes bf16 inputs after rounding them (bench/run.py:51-65).
+    assert sha256(quantized(values, dtype)) == case["values_sha256"]
+    program = Compiler().compile(ProgramSpec(op, dtype, case["d"], case["offsets_dtype"]), artifact_cache)
+    methods = case["methods"]
+    envelope = max(m["max_fraction_of_tolerance"] for m in methods.values())
+    expectation = oracle.Expectation(quantized(values, dtype), offsets, operation=op, input_dtype=dtype)
+    for select in ("auto", "classified", "naive"):
+        actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select=select)
+        stats = expectation.check(actual)
+        print(f"{case['source']} {select}: ours {stats['max_abs_error']:.3g} / {stats['max_fraction_of_tolerance']:.3g}"
+              f", reference ragged-auto {methods['ragged-auto']['max_abs_error']:.3g} / "
+              f"{methods['ragged-auto']['max_fraction_of_tolerance']:.3g}, envelope {envelope:.3g}")
+        assert stats["finite_values"] == methods["ragged-auto"]["finite_values"]
+        assert stats["nan_values"] == methods["ragged-auto"]["nan_values"]
+        if op == "max":
+            assert stats["max_abs_error"] == 0.0
+        else:
+            assert stats["max_fraction_of_tolerance"] <= 1.5 * envelope + 1e-9
+        if op == "softmax" and dtype == "bf16":
+            assert stats["max_fraction_of_tolerance"] <= 1.05 * methods["ragged-auto"]["max_fraction_of_tolerance"]

@@ -333,3 +333,38 @@ def test_workspace_contents_do_not_matter(artifact_cache, op, dtype, d):
         for workspace in program._workspaces.values():
             workspace.fill_(255)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("d,dtype,masked", [(1, "f32", False), (2, "bf16", True), (4, "bf16", False)])
+def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
+    """A split part whose wait for its segment's statistics runs out writes
+    nothing and is normalised by the worker's last workgroup. A zero wait
+    limit (set from the host) sends every part that does not find its
+    statistics at once down that path: the same bits as the default run,
+    every segment written once."""
+    spec = native.make_spec("softmax", dtype, "i64", d)
+    t_block, part_rows = spec.t_block, spec.part_rows
+    rng = np.random.default_rng(23 + d)
+    long = rng.integers(t_block + 1, t_block + 6 * part_rows, size=12)
+    lengths = rng.permutation(np.concatenate([long, rng.integers(0, 300, size=2000)])).astype(np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    kwargs = dict(mask=True, scale=1.25) if masked else {}
+    mask = rng.normal(size=values.shape).astype(np.float32) if masked else None
+    program = program_for(artifact_cache, "softmax", dtype, d, "i64", debug_visits=True, **kwargs)
+    assert not program.metadata["fused"]
+    baseline, _ = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified", mask=mask,
+                              debug_buffers={})
+    module = program._module(0)
+    try:
+        module.set_spin_limit(0)
+        buffers = {}
+        actual, _ = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified",
+                                mask=mask, debug_buffers=buffers)
+    finally:
+        module.set_spin_limit(-1)
+    np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
+    deferred = int(buffers["class_counts"].cpu().numpy()[5])
+    print(f"split parts deferred to the last workgroup: {deferred}")
+    check(actual, values, offsets, op="softmax", dtype=dtype, mask=mask, scale=1.25 if masked else 1.0)
+    assert np.array_equal(actual, baseline, equal_nan=True)
