@@ -199,6 +199,27 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
            void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Size of the static workspace rg_run_static uses on each device (64 MiB). */
+#define RG_STATIC_WORKSPACE_BYTES (64ull << 20)
+
+/* rg_run without a caller workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference: its
+ * runtime always allocates scratch per call (runtime.py:538-542).
+ *
+ * The workspace is a static device array of RG_STATIC_WORKSPACE_BYTES per
+ * device, held from the first rg_module_create on that device until the
+ * process ends. Plans whose workspace_bytes exceed it fail with
+ * RG_E_WORKSPACE before anything is launched (rg_run takes any size). Every
+ * call on a device shares that device's array, and each call initialises
+ * every counter and table its kernels read, so no contents carry over;
+ * calls that overlap on one device (two streams, or two host threads) race
+ * on the array and must be serialised by the caller. Calls no allocating
+ * routine: no hipMalloc, no event creation (rg_profile_* does not record
+ * these calls). Same kernels and results as rg_run. Enqueue only. */
+int rg_run_static(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
+                  void* out, const float* mask, void* stream);
+
 /* Longest wait, in microseconds, of every softmax wait for statistics that
  * other workgroups publish, before the work is deferred: a register-resident
  * chunk's wait for the rest of its segment (default 2000; deferred chunks

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -104,7 +105,40 @@ int combine_features_host(int d) { return next_pow2_capped(d, rg::kCombineFeatur
 bool mul_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_mul_overflow(a, b, out) && *out >= 0; }
 bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow(a, b, out) && *out >= 0; }
 
+// Workspace of the allocation-free entry point (rg_run_static): one array
+// per device, held by the loaded code object until the process ends. Host
+// code never passes `scratch` itself to a kernel or a copy: its host-side
+// name is not a device address. Its device address is resolved once per
+// device with hipGetSymbolAddress (set_up_static_scratch, called by
+// rg_module_create with that device current) and only that address is used.
+constexpr uint64_t kStaticScratchBytes = RG_STATIC_WORKSPACE_BYTES;
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch[kMaxDevices];          // device address of `scratch` on each device, or null
+
 }  // namespace
+
+static __device__ __align__(256) unsigned char scratch[RG_STATIC_WORKSPACE_BYTES];
+
+// Resolve `scratch` on the current device `device` (once); RG_OK or the HIP error.
+static int set_up_static_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail(RG_E_INVALID, "device ordinal %d out of range", device);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[device]) return RG_OK;
+  void* address = nullptr;
+  const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+  if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
+  if (!address || (reinterpret_cast<uintptr_t>(address) & (kAlign - 1)) != 0)
+    return fail(RG_E_DEVICE, "static workspace of device %d is not 256-byte aligned", device);
+  g_scratch[device] = address;
+  return RG_OK;
+}
+
+static void* static_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  return g_scratch[device];
+}
 
 // Event pool of a profiling session: launches+1 events per recorded call.
 struct Profile {
@@ -263,6 +297,14 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
   if (err != hipSuccess) {
     delete module;
     return hip_fail(err, "hipSetDevice");
+  }
+  // The allocation-free entry point's workspace on this device (the device
+  // is current here).
+  const int scratch_status = set_up_static_scratch(device);
+  if (scratch_status != RG_OK) {
+    (void)hipSetDevice(previous);
+    delete module;
+    return scratch_status;
   }
   int clock_khz = 0;
   if (err == hipSuccess) err = hipDeviceGetAttribute(&clock_khz, hipDeviceAttributeWallClockRate, device);
@@ -510,7 +552,7 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
 
 }  // extern "C"
 
-// Enqueue `plan` with `workspace` (rg_run). `profiled`: the
+// Enqueue `plan` with `workspace` (rg_run, rg_run_static). `profiled`: the
 // call may record HIP events (rg_profile_start), which creates them; the
 // allocation-free entry point passes false.
 static int enqueue(const char* entry, const rg_module* module, const rg_plan* plan, const void* values,
@@ -621,6 +663,20 @@ extern "C" {
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets, void* out,
            const float* mask, void* workspace, uint64_t workspace_bytes, void* stream) {
   return enqueue("rg_run", module, plan, values, offsets, out, mask, workspace, workspace_bytes, stream, true);
+}
+
+int rg_run_static(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets, void* out,
+                  const float* mask, void* stream) {
+  if (!module || !plan) return fail(RG_E_INVALID, "rg_run_static: null module or plan");
+  if (plan->workspace_bytes > kStaticScratchBytes)
+    return fail(RG_E_WORKSPACE,
+                "rg_run_static: the plan needs %llu bytes of workspace; the static workspace holds at most %llu "
+                "(use rg_run with a caller-allocated workspace)",
+                (unsigned long long)plan->workspace_bytes, (unsigned long long)kStaticScratchBytes);
+  void* base = static_scratch(module->device);
+  if (!base) return fail(RG_E_DEVICE, "rg_run_static: no static workspace address for device %d", module->device);
+  return enqueue("rg_run_static", module, plan, values, offsets, out, mask, plan->workspace_bytes ? base : nullptr,
+                 plan->workspace_bytes, stream, false);
 }
 
 int rg_check_offsets(int device, int offsets_dtype, const void* offsets, int64_t n, int64_t b, int64_t min_len,

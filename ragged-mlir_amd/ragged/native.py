@@ -28,6 +28,7 @@ BUFFERS = ("class_counts", "segment_ids", "item_segments", "part_begin", "partia
            "max_stats", "sum_stats", "visits", "deferred", "arrive", "segment_arrive", "items", "block_items",
            "pairs", "final_pairs")
 MAX_LAUNCHES = 8
+STATIC_WORKSPACE_BYTES = 64 << 20    # RG_STATIC_WORKSPACE_BYTES
 
 RG_OK, RG_E_INVALID, RG_E_DEVICE, RG_E_UNSUPPORTED, RG_E_WORKSPACE = 0, -1, -2, -3, -4
 
@@ -85,6 +86,7 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         "rg_module_resident": (c_int, [vp, c_int, ctypes.POINTER(c_i64)]),
         "rg_plan_create": (c_int, [vp, c_i64, c_i64, c_int, ctypes.POINTER(Plan)]),
         "rg_run": (c_int, [vp, ctypes.POINTER(Plan), vp, vp, vp, vp, vp, c_u64, vp]),
+        "rg_run_static": (c_int, [vp, ctypes.POINTER(Plan), vp, vp, vp, vp, vp]),
         "rg_check_offsets": (c_int, [c_int, c_int, vp, c_i64, c_i64, c_i64, c_i64, vp, vp]),
         "rg_profile_start": (c_int, [vp, c_int]),
         "rg_module_set_spin_limit": (c_int, [vp, c_i64]),
@@ -215,6 +217,14 @@ class NativeModule:
                                   stream)
         if status:
             _check(status, "rg_run")
+
+    def run_static(self, plan: Plan, values: int, offsets: int, out: int, mask: int | None, stream: int) -> None:
+        """``rg_run_static``: the plan on the library's static per-device
+        workspace (no allocation; plans up to STATIC_WORKSPACE_BYTES; calls
+        that overlap on one device race)."""
+        status = self._lib.rg_run_static(self._handle, plan_ref(plan), values, offsets, out, mask, stream)
+        if status:
+            _check(status, "rg_run_static")
 
     def set_spin_limit(self, microseconds: int) -> None:
         """Bound of every softmax wait for other workgroups' statistics: a
