@@ -8,13 +8,13 @@ in ``libragged_hip.so`` (C ABI: include/ragged_hip.h). Torch and the native
 library load lazily; nothing here falls back to the CPU.
 """
 from .cache import Artifact, ArtifactCache, CacheKey
-from .compiler import Compiler
+from .compiler import CompilationResult, Compiler
 from .errors import (CacheError, CacheMismatch, CacheMiss, CompilationError, RaggedError, RuntimeUnavailable,
                      SpecializationLimit, ToolchainUnavailable, ValidationError)
 from .model import DIALECT_VERSION, ExecutionReport, Hints, Optimizations, ProgramSpec
 from .runtime import CompiledProgram
 
-__all__ = ["Artifact", "ArtifactCache", "CacheKey", "Compiler", "CompiledProgram", "DIALECT_VERSION",
+__all__ = ["Artifact", "ArtifactCache", "CacheKey", "CompilationResult", "Compiler", "CompiledProgram", "DIALECT_VERSION",
            "ExecutionReport", "Hints", "Optimizations", "ProgramSpec", "RaggedError", "ValidationError",
            "CacheError", "CacheMismatch", "CacheMiss", "CompilationError", "RuntimeUnavailable",
            "SpecializationLimit", "ToolchainUnavailable"]

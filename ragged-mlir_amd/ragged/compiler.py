@@ -12,19 +12,30 @@ different code therefore misses the cache instead of reusing stale metadata.
 """
 from __future__ import annotations
 
-from dataclasses import replace
+from dataclasses import dataclass, replace
 import json
 import os
 from pathlib import Path
 from typing import Any
 
 from . import native
-from .cache import Artifact, ArtifactCache, CacheKey, _unique_object
+from .cache import Artifact, ArtifactCache, CacheKey, parse_strict_json
 from .errors import CacheMismatch, CacheMiss, CompilationError, RuntimeUnavailable, ToolchainUnavailable
 from .model import DIALECT_VERSION, ProgramSpec, canonical_json
 from .validation import build_manifest, validate_manifest
 
 TOOLCHAIN_FIELDS = ("library_sha256", "build_info", "abi_version", "dialect_version", "chip")
+EMITS = ("legal", "plan", "gpu", "nvvm", "ptx", "cubin")
+
+
+@dataclass(frozen=True)
+class CompilationResult:
+    """One lowering stage of a spec (reference compiler.py:24-28): its bytes,
+    diagnostics, the stage name and the command that produced it."""
+    output: bytes
+    diagnostics: str
+    emit: str
+    command: tuple[str, ...]
 
 
 class Compiler:
@@ -42,7 +53,7 @@ class Compiler:
     @staticmethod
     def _load_record(path: Path) -> dict[str, Any]:
         try:
-            data = json.loads(path.read_text(encoding="utf-8"), object_pairs_hook=_unique_object)
+            data = parse_strict_json(path.read_text(encoding="utf-8"))
         except (OSError, ValueError, UnicodeError) as exc:
             raise ToolchainUnavailable(f"cannot read toolchain record {path}: {exc}") from exc
         if (not isinstance(data, dict) or set(data) != {"schema", "toolchain"} or data["schema"] != 2
@@ -72,6 +83,55 @@ class Compiler:
         Path(path).write_text(json.dumps(data, indent=2, sort_keys=True) + "\n", encoding="utf-8")
         return data
 
+    @staticmethod
+    def _manifest(spec: ProgramSpec, toolchain: dict[str, Any]) -> dict[str, Any]:
+        """The manifest an artifact of ``spec`` records: the library's class
+        thresholds and part size for it, and whether softmax runs
+        register-resident with those effective thresholds."""
+        defaults = native.make_spec(spec.op, spec.dtype, spec.offsets_dtype, spec.feature_dim, scale=spec.scale,
+                                    mask=spec.mask, vectorize=spec.optimizations.vectorize,
+                                    debug_visits=spec.debug_visits)
+        metadata = build_manifest(spec, thresholds=(int(defaults.t_wave), int(defaults.t_block)),
+                                  part_rows=int(defaults.part_rows), library_sha256=toolchain["library_sha256"],
+                                  build_info=toolchain["build_info"])
+        if metadata["thresholds"]:
+            # Optimizations can move the thresholds; the register-resident
+            # softmax depends on the effective ones.
+            effective = native.make_spec(spec.op, spec.dtype, spec.offsets_dtype, spec.feature_dim,
+                                         scale=spec.scale, mask=spec.mask, vectorize=spec.optimizations.vectorize,
+                                         debug_visits=spec.debug_visits, t_wave=metadata["thresholds"][0],
+                                         t_block=metadata["thresholds"][1], part_rows=metadata["part_rows"])
+            if native.uses_fused(effective):
+                metadata = build_manifest(spec, thresholds=tuple(metadata["thresholds"]),
+                                          part_rows=metadata["part_rows"], library_sha256=toolchain["library_sha256"],
+                                          build_info=toolchain["build_info"], fused=True)
+        return metadata
+
+    def lower(self, spec: ProgramSpec, *, emit: str = "gpu", explain: bool = False,
+              features: str = "gfx950") -> CompilationResult:
+        """The reference's staged lowering (compiler.py:114-144). Its stages
+        that exist here: ``legal`` is the spec's canonical source text (what
+        its ir_hash covers) and ``plan`` the manifest ``compile`` publishes
+        (kernels, classes, thresholds, workspace layout rule). The MLIR/NVVM
+        stages (gpu, nvvm, ptx, cubin) have no counterpart: the gfx950
+        kernels are compiled ahead of time into libragged_hip.so, so they
+        raise CompilationError. ``explain`` adds the stage's rationale to the
+        diagnostics; ``features`` is recorded in the command."""
+        if emit not in EMITS:
+            raise ValueError("emit must be legal, plan, gpu, nvvm, ptx or cubin")
+        command = (native.LIBRARY_PATH.name, f"--emit={emit}", f"--chip={spec.chip}", f"--features={features}") + \
+            (("--explain",) if explain else ())
+        if emit == "legal":
+            text = spec.source_text()
+            notes = "canonical source text of the specialisation (sha256 = ir_hash)" if explain else ""
+            return CompilationResult(text.encode(), notes, emit, command)
+        if emit == "plan":
+            metadata = self._manifest(spec, self.toolchain())
+            notes = "kernels, classes and thresholds the published artifact records" if explain else ""
+            return CompilationResult((canonical_json(metadata) + "\n").encode(), notes, emit, command)
+        raise CompilationError(f"--emit={emit} has no counterpart in this build: there is no MLIR/NVVM lowering, "
+                               "the gfx950 kernels are compiled ahead of time into libragged_hip.so")
+
     def compile(self, spec: ProgramSpec, cache: ArtifactCache, *, adaptive: bool = True):
         """Resolve (or load) the artifact of ``spec``; with ``adaptive`` a
         classifying program also gets its block-per-segment companion."""
@@ -95,23 +155,7 @@ class Compiler:
             if self.record is not None:
                 raise CacheMiss(f"{spec.signature} {spec.strategy} ({spec.ir_hash[:16]}) was not precompiled into "
                                 f"{cache.root}; a toolchain-record Compiler builds nothing") from None
-        defaults = native.make_spec(spec.op, spec.dtype, spec.offsets_dtype, spec.feature_dim, scale=spec.scale,
-                                    mask=spec.mask, vectorize=spec.optimizations.vectorize,
-                                    debug_visits=spec.debug_visits)
-        metadata = build_manifest(spec, thresholds=(int(defaults.t_wave), int(defaults.t_block)),
-                                  part_rows=int(defaults.part_rows), library_sha256=toolchain["library_sha256"],
-                                  build_info=toolchain["build_info"])
-        if metadata["thresholds"]:
-            # Whether softmax runs register-resident depends on the effective
-            # thresholds (optimizations can move them).
-            effective = native.make_spec(spec.op, spec.dtype, spec.offsets_dtype, spec.feature_dim,
-                                         scale=spec.scale, mask=spec.mask, vectorize=spec.optimizations.vectorize,
-                                         debug_visits=spec.debug_visits, t_wave=metadata["thresholds"][0],
-                                         t_block=metadata["thresholds"][1], part_rows=metadata["part_rows"])
-            if native.uses_fused(effective):
-                metadata = build_manifest(spec, thresholds=tuple(metadata["thresholds"]),
-                                          part_rows=metadata["part_rows"], library_sha256=toolchain["library_sha256"],
-                                          build_info=toolchain["build_info"], fused=True)
+        metadata = self._manifest(spec, toolchain)
         validate_manifest(metadata)
         code = (canonical_json({"library": native.LIBRARY_PATH.name, **toolchain}) + "\n").encode()
         # Bind the manifest to its source before publication.

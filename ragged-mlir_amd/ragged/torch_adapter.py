@@ -3,19 +3,27 @@
 Same public surface as the reference's ``python/ragged/torch_adapter.py``
 (:19-180): ``register_program``, ``register_torch_ops``, ``segment_reduce``,
 ``segment_softmax``, ``bind``, ``jagged_components``, ``njt_reduce`` and
-``njt_softmax``, and the two custom-op schemas (:57-58, :72-73):
+``njt_softmax``, and the reference's two custom-op schemas exactly
+(:57-58, :72-73):
 
     ragged_mlir::segment_reduce(Tensor values, Tensor offsets, str kind, str program,
-                                str mode="validated", int? max_len=None) -> Tensor
+                                str mode="validated") -> Tensor
     ragged_mlir::segment_softmax(Tensor values, Tensor offsets, str program,
-                                 str mode="validated", Tensor? mask=None, int? max_len=None) -> Tensor
+                                 str mode="validated", Tensor? mask=None) -> Tensor
 
 ``program`` is the token ``register_program`` returns (the artifact digest).
 The ops are opaque and forward-only; their fake implementations check shapes
 and dtypes only, so they trace under ``torch.compile`` without reading
-offsets. The trailing ``max_len`` (absent in the reference's schemas, which
-calls positionally still match) carries the caller's longest segment to the
-cost model; the NJT helpers pass the nested tensor's cached ``max_seqlen``.
+offsets. A caller that knows its longest segment (an NJT's cached
+``max_seqlen``) passes it to the cost model through two further ops of this
+build, with ``int max_len`` after ``program``:
+
+    ragged_mlir::segment_reduce_bounded(Tensor values, Tensor offsets, str kind, str program,
+                                        int max_len, str mode="validated") -> Tensor
+    ragged_mlir::segment_softmax_bounded(Tensor values, Tensor offsets, str program, int max_len,
+                                         str mode="validated", Tensor? mask=None) -> Tensor
+
+The helpers below pick the bounded op whenever ``max_len`` is given.
 Importing ``ragged`` does not import torch: call ``register_torch_ops()``
 (the helpers do) to register.
 """
@@ -110,6 +118,27 @@ def _reduce_kind(kind: str) -> str:
     return kind
 
 
+def _bound(max_len) -> int:
+    if type(max_len) is not int or max_len < 0:
+        raise ValidationError("max_len must be a nonnegative int")
+    return max_len
+
+
+def _reduce_fake(values, offsets, kind, mode, torch):
+    _mode(mode)
+    _reduce_kind(kind)
+    _check_shapes(values, offsets, torch)
+    return values.new_empty((offsets.shape[0] - 1, values.shape[1]))
+
+
+def _softmax_fake(values, offsets, mode, mask, torch):
+    _mode(mode)
+    _check_shapes(values, offsets, torch)
+    if mask is not None:
+        _check_mask_shape(values, mask, torch)
+    return values.new_empty(values.shape)
+
+
 def register_torch_ops() -> dict[str, Any]:
     """Register both custom ops once per process; returns them by name."""
     with _lock:
@@ -119,49 +148,74 @@ def register_torch_ops() -> dict[str, Any]:
 
         @torch.library.custom_op("ragged_mlir::segment_reduce", mutates_args=(),
                                  schema="(Tensor values, Tensor offsets, str kind, str program, "
-                                        "str mode=\"validated\", int? max_len=None) -> Tensor")
-        def segment_reduce_op(values, offsets, kind, program, mode="validated", max_len=None):
-            return _run(values, offsets, program, _reduce_kind(kind), mode, max_len=max_len)
+                                        "str mode=\"validated\") -> Tensor")
+        def segment_reduce_op(values, offsets, kind, program, mode="validated"):
+            return _run(values, offsets, program, _reduce_kind(kind), mode)
 
         @segment_reduce_op.register_fake
-        def _(values, offsets, kind, program, mode="validated", max_len=None):
-            _mode(mode)
-            _reduce_kind(kind)
-            _check_shapes(values, offsets, torch)
-            return values.new_empty((offsets.shape[0] - 1, values.shape[1]))
+        def _(values, offsets, kind, program, mode="validated"):
+            return _reduce_fake(values, offsets, kind, mode, torch)
 
         @torch.library.custom_op("ragged_mlir::segment_softmax", mutates_args=(),
                                  schema="(Tensor values, Tensor offsets, str program, str mode=\"validated\", "
-                                        "Tensor? mask=None, int? max_len=None) -> Tensor")
-        def segment_softmax_op(values, offsets, program, mode="validated", mask=None, max_len=None):
-            return _run(values, offsets, program, "softmax", mode, mask, max_len)
+                                        "Tensor? mask=None) -> Tensor")
+        def segment_softmax_op(values, offsets, program, mode="validated", mask=None):
+            return _run(values, offsets, program, "softmax", mode, mask)
 
         @segment_softmax_op.register_fake
-        def _(values, offsets, program, mode="validated", mask=None, max_len=None):
-            _mode(mode)
-            _check_shapes(values, offsets, torch)
-            if mask is not None:
-                _check_mask_shape(values, mask, torch)
-            return values.new_empty(values.shape)
+        def _(values, offsets, program, mode="validated", mask=None):
+            return _softmax_fake(values, offsets, mode, mask, torch)
+
+        @torch.library.custom_op("ragged_mlir::segment_reduce_bounded", mutates_args=(),
+                                 schema="(Tensor values, Tensor offsets, str kind, str program, int max_len, "
+                                        "str mode=\"validated\") -> Tensor")
+        def segment_reduce_bounded_op(values, offsets, kind, program, max_len, mode="validated"):
+            return _run(values, offsets, program, _reduce_kind(kind), mode, max_len=_bound(max_len))
+
+        @segment_reduce_bounded_op.register_fake
+        def _(values, offsets, kind, program, max_len, mode="validated"):
+            _bound(max_len)
+            return _reduce_fake(values, offsets, kind, mode, torch)
+
+        @torch.library.custom_op("ragged_mlir::segment_softmax_bounded", mutates_args=(),
+                                 schema="(Tensor values, Tensor offsets, str program, int max_len, "
+                                        "str mode=\"validated\", Tensor? mask=None) -> Tensor")
+        def segment_softmax_bounded_op(values, offsets, program, max_len, mode="validated", mask=None):
+            return _run(values, offsets, program, "softmax", mode, mask, _bound(max_len))
+
+        @segment_softmax_bounded_op.register_fake
+        def _(values, offsets, program, max_len, mode="validated", mask=None):
+            _bound(max_len)
+            return _softmax_fake(values, offsets, mode, mask, torch)
 
         _ops["segment_reduce"] = segment_reduce_op
         _ops["segment_softmax"] = segment_softmax_op
+        _ops["segment_reduce_bounded"] = segment_reduce_bounded_op
+        _ops["segment_softmax_bounded"] = segment_softmax_bounded_op
         return dict(_ops)
 
 
 def segment_reduce(values, offsets, kind: str, *, program: CompiledProgram, mode: str = "validated",
                    max_len: int | None = None):
-    """``kind`` ("sum" / "max") of every segment through the custom op."""
+    """``kind`` ("sum" / "max") of every segment through the custom op (the
+    bounded one when ``max_len`` is given)."""
     ops = register_torch_ops()
-    return ops["segment_reduce"](values, offsets, kind, register_program(program), mode, max_len)
+    token = register_program(program)
+    if max_len is None:
+        return ops["segment_reduce"](values, offsets, kind, token, mode)
+    return ops["segment_reduce_bounded"](values, offsets, kind, token, max_len, mode)
 
 
 def segment_softmax(values, offsets, *, program: CompiledProgram, mode: str = "validated", mask=None,
                     max_len: int | None = None):
-    """Softmax of every segment through the custom op."""
+    """Softmax of every segment through the custom op (the bounded one when
+    ``max_len`` is given)."""
     _mask_matches(program.spec.mask, mask)
     ops = register_torch_ops()
-    return ops["segment_softmax"](values, offsets, register_program(program), mode, mask, max_len)
+    token = register_program(program)
+    if max_len is None:
+        return ops["segment_softmax"](values, offsets, token, mode, mask)
+    return ops["segment_softmax_bounded"](values, offsets, token, max_len, mode, mask)
 
 
 def bind(program: CompiledProgram, *, mode: str = "validated"):
@@ -172,18 +226,22 @@ def bind(program: CompiledProgram, *, mode: str = "validated"):
     ops = register_torch_ops()
     token = register_program(program)
     if program.spec.op == "softmax":
-        softmax = ops["segment_softmax"]
+        softmax, softmax_bounded = ops["segment_softmax"], ops["segment_softmax_bounded"]
         has_mask = program.spec.mask
 
         def run_softmax(values, offsets, mask=None, max_len=None):
             _mask_matches(has_mask, mask)
-            return softmax(values, offsets, token, mode, mask, max_len)
+            if max_len is None:
+                return softmax(values, offsets, token, mode, mask)
+            return softmax_bounded(values, offsets, token, max_len, mode, mask)
         return run_softmax
-    reduce_ = ops["segment_reduce"]
+    reduce_, reduce_bounded = ops["segment_reduce"], ops["segment_reduce_bounded"]
     kind = program.spec.op
 
     def run_reduce(values, offsets, max_len=None):
-        return reduce_(values, offsets, kind, token, mode, max_len)
+        if max_len is None:
+            return reduce_(values, offsets, kind, token, mode)
+        return reduce_bounded(values, offsets, kind, token, max_len, mode)
     return run_reduce
 
 

@@ -4,6 +4,11 @@ Restates simon-jd/ragged-mlir ``bench/distributions.py`` (length
 distributions with exact integer allocation to a fixed N) and the value
 generation of ``bench/run.py:51-65``, and defines the five measured
 configurations (C1-C5) this package is benchmarked on. NumPy only; no torch.
+
+``allocate``, ``make_lengths``, ``offsets_from_lengths`` and ``describe``
+follow the reference's algorithm step for step (they must reproduce its
+recorded inputs bit for bit): Copyright (c) 2026 Junrui Duan, MIT License
+(NOTICE.md).
 """
 from __future__ import annotations
 

@@ -106,3 +106,21 @@ def test_njt_contract_rejections():
         jagged_components(holes)
     with pytest.raises(ValidationError, match="\\[B, jagged, D\\]"):
         jagged_components(torch.nested.nested_tensor_from_jagged(torch.randn(6), offsets=torch.tensor([0, 2, 6])))
+
+
+def test_reference_schemas_are_exact(ops):
+    """The reference's two schemas (torch_adapter.py:57-58, 72-73) unchanged;
+    max_len travels through the bounded ops of this build."""
+    assert str(ops["segment_reduce"]._opoverload._schema) == (
+        'ragged_mlir::segment_reduce(Tensor values, Tensor offsets, str kind, str program, '
+        'str mode="validated") -> Tensor')
+    assert str(ops["segment_softmax"]._opoverload._schema) == (
+        'ragged_mlir::segment_softmax(Tensor values, Tensor offsets, str program, str mode="validated", '
+        'Tensor? mask=None) -> Tensor')
+    out = ops["segment_reduce_bounded"](meta((17, 13)), meta((5,), torch.int64), "sum", "no-program", 9)
+    assert out.shape == (4, 13)
+    out = ops["segment_softmax_bounded"](meta((9, 4)), meta((3,), torch.int64), "no-program", 9, "checked",
+                                         meta((9, 4)))
+    assert out.shape == (9, 4)
+    with pytest.raises(ValidationError, match="max_len"):
+        ops["segment_reduce_bounded"](meta((17, 13)), meta((5,), torch.int64), "sum", "no-program", -1)
