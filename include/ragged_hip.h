@@ -50,7 +50,8 @@ enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1, RG_SHORT_SEGMENT
 
 /* Kernel roles, in launch order of the classified schedule. */
 enum rg_role {
-  RG_ROLE_INIT = 0,
+  RG_ROLE_INIT = 0,            /* register-resident softmax only: pair slots; otherwise
+                                  k_classify initialises what a call uses */
   RG_ROLE_CLASSIFY = 1,
   RG_ROLE_WAVE = 2,            /* not launched: the wave class runs inside RG_ROLE_WORKER */
   RG_ROLE_BLOCK = 3,           /* not launched: the block class runs inside RG_ROLE_WORKER */
@@ -129,10 +130,11 @@ enum rg_buffer {
                                (register-resident softmax chunks, or worker softmax split
                                parts), 6 tree items; 7 slot 0's count for a register-resident
                                softmax (whose slot 0 stays 0); 8 the rest of the wave class;
-                               9 softmax split-part normalisation ticket; 10 unused; 11 worker
-                               softmax workgroups finished; then 16 ticket counters of the
-                               classified worker, 256 bytes apart from byte 256 (4352 bytes
-                               in all) */
+                               9 softmax split-part normalisation ticket; 10 unused; 11 done
+                               lanes finished (of the call's last kernel); then 16 ticket
+                               counters of the classified worker and 16 done lanes, 256 bytes
+                               apart from byte 256 (8448 bytes in all). All zero before a
+                               call; the call's last workgroup leaves them zero. */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class; the wave class holds
                                its segments of at most alone_rows rows from the front and the
                                others from the back */
@@ -195,7 +197,14 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
 /* Enqueue the plan on `stream` (a hipStream_t); replaces run_plan
  * (Driver.cpp:299-353). `workspace` must hold plan->workspace_bytes bytes
  * at a 256-byte aligned address (may be NULL when that is 0); `mask` is NULL
- * unless the module has one. */
+ * unless the module has one.
+ *
+ * Workspace contract: zero-filled before its first call. Every call
+ * initialises the per-segment state it uses and its last workgroup returns
+ * the workspace's counters to zero, so calls in order on one stream reuse it
+ * with no clearing (a failed rg_run may leave it dirty: zero it again). A
+ * module with debug_visits keeps its counters for inspection instead: give
+ * each of its calls a zeroed workspace. */
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
            void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
 
@@ -216,7 +225,8 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
  * calls that overlap on one device (two streams, or two host threads) race
  * on the array and must be serialised by the caller. Calls no allocating
  * routine: no hipMalloc, no event creation (rg_profile_* does not record
- * these calls). Same kernels and results as rg_run. Enqueue only. */
+ * these calls). Same kernels and results as rg_run; a debug_visits module
+ * is refused (it keeps its counters after a call). Enqueue only. */
 int rg_run_static(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
                   void* out, const float* mask, void* stream);
 

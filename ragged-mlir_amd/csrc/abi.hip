@@ -113,6 +113,7 @@ bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow
 // rg_module_create with that device current) and only that address is used.
 constexpr uint64_t kStaticScratchBytes = RG_STATIC_WORKSPACE_BYTES;
 constexpr int kMaxDevices = 64;
+constexpr size_t kScratchCounterBytes = (size_t)rg::kTicketStride * 8 * (1 + 2 * rg::kTicketLanes);
 std::mutex g_scratch_mutex;
 void* g_scratch[kMaxDevices];          // device address of `scratch` on each device, or null
 
@@ -130,6 +131,11 @@ static int set_up_static_scratch(int device) {
   if (err != hipSuccess) return hip_fail(err, "hipGetSymbolAddress(scratch)");
   if (!address || (reinterpret_cast<uintptr_t>(address) & (kAlign - 1)) != 0)
     return fail(RG_E_DEVICE, "static workspace of device %d is not 256-byte aligned", device);
+  // A workspace is all-zero before its first call (every call leaves its
+  // counters at zero again); the loader zero-fills the array, this makes
+  // sure of the counter region.
+  const hipError_t zero = hipMemset(address, 0, kScratchCounterBytes);
+  if (zero != hipSuccess) return hip_fail(zero, "hipMemset(static workspace counters)");
   g_scratch[device] = address;
   return RG_OK;
 }
@@ -280,6 +286,9 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
     delete module;
     return fail(RG_E_INVALID, "no compiled kernel for this dtype/feature geometry");
   }
+  // k_init runs only before the register-resident softmax (its pair slots);
+  // otherwise k_classify initialises what a call uses. Every classified
+  // call's last workgroup returns the counters to zero.
   module->roles[RG_ROLE_INIT] = rg::kernel_init();
   module->roles[RG_ROLE_CLASSIFY] = rg::kernel_classify(spec.offsets_dtype);
   module->roles[RG_ROLE_WORKER] = k.worker;
@@ -493,7 +502,7 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   int64_t stat_bytes, item_bytes;
   if (!mul_ok(items_cap, (int64_t)d * 4, &item_bytes) || !mul_ok(b_split, (int64_t)d * 4, &stat_bytes))
     return fail(RG_E_INVALID, "split workspace bytes overflow");
-  sizes[RG_BUF_COUNTERS] = (int64_t)rg::kTicketStride * 8 * (1 + rg::kTicketLanes);
+  sizes[RG_BUF_COUNTERS] = (int64_t)rg::kTicketStride * 8 * (1 + 2 * rg::kTicketLanes);
   if (!module->fused) {
     // Part arrivals per split segment (the worker's last part combines).
     if (!mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE])) return fail(RG_E_INVALID, "arrival bytes overflow");
@@ -529,10 +538,10 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   }
   plan->workspace_bytes = (uint64_t)end;
 
-  // k_init is grid-stride: enough workgroups for the sentinel fill of the
-  // register-resident softmax (8 slots per thread), one for a plain reset.
-  const int64_t init_work = module->fused ? items_cap * d : 0;
-  add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, init_work / (rg::kBlock * 8))), 1);
+  if (module->fused) {
+    // Grid-stride fill of every pair slot (8 per thread).
+    add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, items_cap * d / (rg::kBlock * 8))), 1);
+  }
   const int classify_block = b >= rg::kClassifyLarge ? rg::kClassifyBlock : rg::kBlock;
   add_launch(RG_ROLE_CLASSIFY, (b + classify_block - 1) / classify_block, 1, classify_block);
   if (module->fused) {
@@ -668,6 +677,9 @@ int rg_run(const rg_module* module, const rg_plan* plan, const void* values, con
 int rg_run_static(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets, void* out,
                   const float* mask, void* stream) {
   if (!module || !plan) return fail(RG_E_INVALID, "rg_run_static: null module or plan");
+  if (module->spec.debug_visits)
+    return fail(RG_E_INVALID, "rg_run_static: a debug_visits module keeps its counters after a call; use rg_run "
+                              "with a zeroed workspace per call");
   if (plan->workspace_bytes > kStaticScratchBytes)
     return fail(RG_E_WORKSPACE,
                 "rg_run_static: the plan needs %llu bytes of workspace; the static workspace holds at most %llu "

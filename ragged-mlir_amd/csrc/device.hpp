@@ -55,6 +55,8 @@ constexpr int kClassifyWaves = kClassifyBlock / kWave;
 constexpr int64_t kClassifyLarge = 16384;
 constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
+constexpr int kTreeGroup = 32;         // register-resident softmax: chunks per first-level tree group
+constexpr int kDoneSlot = 11;          // counters slot: workgroups of the call's last kernel finished
 constexpr int32_t kStatsReady = -1;     // seg_arrive[k] once a split segment's softmax statistics are published
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
@@ -63,13 +65,31 @@ __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 // IEEE-754 maximum: NaN if either operand is NaN (v_maximum3_f32 on gfx950).
 __device__ __forceinline__ float fmax_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
+// exp(x) to 1.25 ulp (measured on MI355X over [-104, 89]) in eight
+// instructions, one of them transcendental: the product x log2(e) is split
+// exactly with fused multiply-adds (p + d, p the f32 product with log2(e)
+// rounded to f32, d the rounding error plus x times the rest of log2(e)),
+// then 2^(p + d) = 2^p (1 + d ln 2), exact to far below an ulp as |d| <
+// 2^-16. __expf rounds x log2(e) to f32 first: 16 ulp at x = -20. ±inf
+// and NaN arguments give 2^p itself (0, inf, NaN).
+constexpr float kLog2eHi = 1.44269502162933349609375f;   // log2(e) rounded to f32
+constexpr float kLog2eLo = 1.925962989091090e-8f;        // log2(e) - kLog2eHi
+constexpr float kLn2 = 0.693147180559945309f;
+__device__ __forceinline__ float exp_split(float x) {
+  const float p = x * kLog2eHi;
+  const float lo = __builtin_fmaf(x, kLog2eHi, -p);
+  const float d = __builtin_fmaf(x, kLog2eLo, lo);
+  const float r = __builtin_amdgcn_exp2f(p);
+  const float y = __builtin_fmaf(r, d * kLn2, r);
+  return __builtin_isfinite(p) ? y : r;
+}
+
 // exp of a softmax output (and of what scales one) for data of type T: f32
-// outputs take the library's accurate expf (about 1 ulp; __expf scales its
-// argument by log2(e) in f32 first, a relative error that grows with
-// |x - m|), bf16 outputs the fast form, far below their rounding.
+// outputs take exp_split, bf16 outputs the fast form, far below their
+// rounding.
 template <class T>
 __device__ __forceinline__ float exp_out(float x) {
-  if constexpr (std::is_same<T, float>::value) return expf(x);
+  if constexpr (std::is_same<T, float>::value) return exp_split(x);
   else return __expf(x);
 }
 // e = exp(x - m) in [0, 1] of bf16 rows held in registers between the two
@@ -137,8 +157,8 @@ struct Params {
                            //      parts (worker softmax); tree items; the wave
                            //      count of a register-resident softmax; the rest
                            //      of the wave class; the split-part normalisation
-                           //      ticket; unused; workgroups finished (worker
-                           //      softmax). Then the worker's ticket lanes
+                           //      ticket; unused; done lanes finished. Then the
+                           //      worker's ticket lanes and the done lanes
                            //      (kTicketStride apart)
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item

@@ -35,7 +35,7 @@
 
 namespace rg {
 
-constexpr int kGroup = 32;          // chunks merged per first-level group
+constexpr int kGroup = kTreeGroup;   // chunks merged per first-level group
 // Sleep between two polls of a waiting chunk, in units of 64 clocks (about
 // 1.7 us at 64). A waiter's fold takes LDS, barriers and issue slots from
 // the workgroups that share its CU; on MI355X, C5 runs 1.5-2% faster at 32
@@ -673,6 +673,14 @@ __device__ __forceinline__ void renormalize_rows(const Params& p, const RowGeo& 
 template <class T, class OffT, int VEC, bool MASK>
 __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
   const int64_t count = p.counters[5] < p.items_cap ? p.counters[5] : p.items_cap;
+  const int64_t n_coop = p.counters[8];
+  const int64_t n_wave = p.counters[7];
+  const int64_t batch = wave_batch_size<false, VEC>(p.d);
+  // Grid-stride over each list: workgroups past the longest list have no
+  // work and leave now, touching no counter (active_workgroups).
+  const int64_t work = max(count, max((n_coop + kWavesPerBlock - 1) / kWavesPerBlock, (n_wave + batch - 1) / batch));
+  const int64_t active = active_workgroups(work);
+  if (blockIdx.x >= active) return;
   const int t = threadIdx.x;
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
   // The register-resident kernel that ran held bf16 rows as loaded (e as
@@ -709,13 +717,13 @@ __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
     if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     __syncthreads();
   }
-  const int64_t n_coop = p.counters[8];
   for (int64_t i = blockIdx.x; i * kWavesPerBlock < n_coop; i += gridDim.x)
     coop_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_coop);
-  const int64_t n_wave = p.counters[7];
-  const int64_t batch = wave_batch_size<false, VEC>(p.d);
   for (int64_t i = blockIdx.x; i * batch < n_wave; i += gridDim.x)
     wave_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_wave, false);
+  // The call's last kernel: its last workgroup returns the counters to zero.
+  __shared__ int flag_s;
+  if (last_out(p, &flag_s, active, false)) reset_counters(p);
 }
 
 }  // namespace rg

@@ -3,14 +3,17 @@
 // Schedules (the same arithmetic in both):
 //  * block per segment ("naive"): grid.x walks segments, one 256-thread
 //    workgroup each (reference: the direct schedule, ToGPU.cpp:1283-1349).
-//  * classified: k_init + k_classify bin every segment by length into a
-//    wave64 queue, a workgroup queue and a split queue (reference:
-//    ToGPU.cpp:901-998, with wave64 thresholds); one persistent worker
-//    (worker.hpp) drains the queues (ToGPU.cpp:999-1045). A split segment is
-//    cut into ceil(L / part_rows) parts -- proportional to its length instead
-//    of the reference's fixed 8 -- each processed by one workgroup; the last
-//    part folds them (ToGPU.cpp:399-472) and, for softmax, the worker
-//    then writes the probabilities (ToGPU.cpp:279-281).
+//  * classified: k_classify bins every segment by length into a wave64
+//    queue, a workgroup queue and a split queue (reference: ToGPU.cpp:
+//    901-998, with wave64 thresholds) and initialises the per-segment state
+//    the call uses; one persistent worker (worker.hpp) drains the queues
+//    (ToGPU.cpp:999-1045), and the call's last workgroup returns the
+//    counters to zero for the next call (last_out, reset_counters). The
+//    register-resident softmax also runs k_init first (its pair slots). A
+//    split segment is cut into ceil(L / part_rows) parts -- proportional to
+//    its length instead of the reference's fixed 8 -- each processed by one
+//    workgroup; the last part folds them (ToGPU.cpp:399-472) and, for
+//    softmax, the worker then writes the probabilities (ToGPU.cpp:279-281).
 #pragma once
 
 #include <type_traits>
@@ -400,18 +403,66 @@ __device__ __forceinline__ int combine_features(int d) {
   return f;
 }
 
+// Workgroups of a persistent grid that take part in a call with `work`
+// units: at most one per unit, at least one (it returns the counters to
+// zero).
+__device__ __forceinline__ int64_t active_workgroups(int64_t work) {
+  const int64_t grid = gridDim.x;
+  return work < 1 ? 1 : (work < grid ? work : grid);
+}
+
+// End of a classified call's last kernel: every active workgroup (blockIdx <
+// `active`, all of whom read the counters first) counts itself out
+// (once its stores are complete when `drain`: what the last workgroup then
+// reads must be published); returns true in the last one. Counting is
+// two-level, because atomics on one address serialise (about 12.5 ns each
+// on MI355X): workgroup w counts at lane w % kTicketLanes (the done lanes,
+// kTicketStride apart after the ticket lanes), the last of each lane at
+// counters[kDoneSlot]. The last workgroup may still use the workspace; it
+// then calls reset_counters.
+__device__ __forceinline__ bool last_out(const Params& p, int* flag_s, int64_t active, bool drain) {
+  if (drain) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this workgroup's stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned count = (unsigned)active;
+    const unsigned lanes = count < (unsigned)kTicketLanes ? count : (unsigned)kTicketLanes;
+    const unsigned lane = blockIdx.x % lanes;
+    const unsigned long long in_lane = (count - lane + lanes - 1) / lanes;   // active workgroups w = lane (mod lanes)
+    unsigned long long* lane_counter = (unsigned long long*)(p.counters + kTicketStride * (1 + kTicketLanes + lane));
+    bool last = false;
+    if (atomicAdd(lane_counter, 1ull) == in_lane - 1)
+      last = atomicAdd((unsigned long long*)(p.counters + kDoneSlot), 1ull) == lanes - 1;
+    *flag_s = last ? 1 : 0;
+  }
+  __syncthreads();
+  return *flag_s != 0;
+}
+
+// Every counter of the workspace back to zero, so the next call's
+// k_classify starts from zero (the workspace's contract: all-zero before its
+// first call, left so by every call). A debug specialisation (visits set)
+// keeps its counters for inspection instead; its workspace is fresh per call.
+__device__ __forceinline__ void reset_counters(const Params& p) {
+  if (p.visits) return;
+  const int t = threadIdx.x;
+  if (t < kTicketStride) p.counters[t] = 0;
+  if (t < 2 * kTicketLanes) p.counters[kTicketStride * (1 + t)] = 0;
+}
+
 #ifdef RG_PROLOGUE_KERNELS
 // Defined in exactly one translation unit (kernels_common.hip).
 
-// Zero the class counters (and the debug visit counts). For the
-// register-resident softmax also: every statistics pair slot gets the
-// unpublished sentinel and every merge counter 0 (grid-stride, coalesced).
+// Register-resident softmax only (the streaming worker's calls need no
+// separate init): zero the class counters, the debug visit counts and the
+// merge counters, and fill every statistics pair slot with the unpublished
+// sentinel (grid-stride, coalesced; the polling merge needs the whole array
+// ready before any chunk publishes).
 __global__ __launch_bounds__(kBlock) void k_init(Params p) {
   const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t threads = (int64_t)gridDim.x * kBlock;
   // Every class counter slot (the first kTicketStride) and every ticket lane.
   if (tid < kTicketStride) p.counters[tid] = 0;
-  if (tid < kTicketLanes) p.counters[kTicketStride * (1 + tid)] = 0;
+  if (tid < 2 * kTicketLanes) p.counters[kTicketStride * (1 + tid)] = 0;   // ticket and done lanes
   if (p.visits) {
     for (int64_t s = tid; s < p.b; s += threads) p.visits[s] = 0;
   }
@@ -454,6 +505,7 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
   // of the wave queue); run 3: the rest of the wave class, one wave each
   // (back of the wave queue); runs 1, 2: block and split classes.
   const int cls = length <= p.t_wave ? (length <= p.alone_rows ? 0 : 3) : (length <= p.t_block ? 1 : 2);
+  if (active && p.visits) p.visits[s] = 0;
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
   // Queue runs: the workgroup (kBlock threads, or kClassifyBlock for many
   // segments) reserves each class's run with one atomic (not one per wave:
@@ -517,6 +569,8 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
         fits = first + parts <= p.items_cap;
       }
       if (p.part_begin) p.part_begin[pos] = first;
+      // The segment's part (or chunk-group) arrivals start at zero.
+      p.seg_arrive[pos] = 0;
     }
     if (p.items) {
       // Item descriptors. An allocation that does not fit the array (only

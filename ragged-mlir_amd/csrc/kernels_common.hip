@@ -1,4 +1,4 @@
-// Op-independent kernels: counter init, classification, checked offsets.
+// Op-independent kernels: pair-slot init, classification, checked offsets.
 #define RG_PROLOGUE_KERNELS
 #include "kernels.hpp"
 #include "table.hpp"

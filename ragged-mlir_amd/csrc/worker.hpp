@@ -571,12 +571,21 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int64_t n_coop = direct ? 0 : p.counters[8];
   const int64_t n_coop_batches = (n_coop + kWavesPerBlock - 1) / kWavesPerBlock;
   const int64_t n_wave = direct ? p.b : p.counters[0];
+  // Every segment reduced alone (all in run 0): the batches take segment ids
+  // in order, as the short-segment schedule does, without the queue.
+  const bool in_order = direct || n_wave == p.b;
   const int64_t n_batches = (n_wave + batch - 1) / batch;
   const int64_t before_alone = n_parts + n_block + n_coop_batches;
   const int64_t total = before_alone + n_batches;
+  // The workgroups that take tickets: at most one per ticket (the grid is
+  // sized to the device, the tickets to the input). The others leave now
+  // and touch no counter -- also when they start after the call's last
+  // workgroup has reset the counters, as they then read no tickets at all.
+  const int64_t active = direct ? gridDim.x : active_workgroups(total);
+  if (blockIdx.x >= active) return;
   // Tickets interleave over the lanes: lane k hands out k, k + lanes, ...
   // to the workgroups blockIdx = k (mod lanes), every lane has at least one.
-  const int lanes = gridDim.x < kTicketLanes ? (int)gridDim.x : kTicketLanes;
+  const int lanes = active < kTicketLanes ? (int)active : kTicketLanes;
   const int lane_id = (int)(blockIdx.x % lanes);
   unsigned long long* counter = (unsigned long long*)(p.counters + kTicketStride * (1 + lane_id));
   int64_t next = blockIdx.x;
@@ -602,15 +611,17 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
     } else if (ticket < before_alone) {
       coop_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - n_parts - n_block, n_coop);
     } else {
-      wave_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - before_alone, n_wave, direct);
+      wave_batch<OP, T, OffT, VEC, FLAT, MASK>(p, ticket - before_alone, n_wave, in_order);
     }
   }
   // Softmax: the split parts' probabilities, from a counter of their own,
   // once this workgroup's tickets have run out (so every part has been
   // handed out). A part whose statistics are not out within drain_ticks is
   // deferred (counters[5] entries of `deferred`, agent scope); the last
-  // workgroup to finish (counters[11]) normalises those: by then every part
-  // has run and every segment's statistics are published.
+  // workgroup out (last_out) normalises those: by then every part has run
+  // and every segment's statistics are published. That workgroup then
+  // returns the counters to zero for the next call.
+  if (direct) return;
   if constexpr (OP == OP_SOFTMAX) {
     if (n_parts > 0) {
       for (;;) {
@@ -626,22 +637,21 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
           if (slot < n_parts) __hip_atomic_store(p.deferred + slot, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
-      // Every store of this workgroup (deferred entries, statistics of the
-      // segments it combined) completes before it counts itself finished.
-      __builtin_amdgcn_s_waitcnt(0x0F70);
-      __syncthreads();
-      if (t == 0) flag_s = atomicAdd((unsigned long long*)(p.counters + 11), 1ull) == gridDim.x - 1;
-      __syncthreads();
-      if (flag_s) {
-        const int64_t deferred = __hip_atomic_load(p.counters + 5, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int64_t count = deferred < n_parts ? deferred : n_parts;
-        for (int64_t j = 0; j < count; ++j) {
-          const int64_t i = __hip_atomic_load(p.deferred + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          (void)normalize_part<T, OffT, VEC, FLAT, MASK>(p, i / tiles_block, (int)(i % tiles_block), false);
-        }
-      }
     }
   }
+  if (!last_out(p, &flag_s, active, OP == OP_SOFTMAX && n_parts > 0)) return;
+  if constexpr (OP == OP_SOFTMAX) {
+    if (n_parts > 0) {
+      const int64_t deferred = __hip_atomic_load(p.counters + 5, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int64_t count = deferred < n_parts ? deferred : n_parts;
+      for (int64_t j = 0; j < count; ++j) {
+        const int64_t i = __hip_atomic_load(p.deferred + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        (void)normalize_part<T, OffT, VEC, FLAT, MASK>(p, i / tiles_block, (int)(i % tiles_block), false);
+      }
+      __syncthreads();
+    }
+  }
+  reset_counters(p);
 }
 
 }  // namespace rg

@@ -150,20 +150,21 @@ class CompiledProgram:
         self._workspaces.clear()
 
     def _workspace(self, torch, device, stream, nbytes: int, fresh: bool):
-        """Scratch of at least ``nbytes`` for a call on ``stream``. Calls on
-        one stream run in order, so they share one allocation (made on that
-        stream); ``fresh`` (debug buffers handed to the caller) allocates a
-        new one."""
+        """Zeroed scratch of at least ``nbytes`` for a call on ``stream``.
+        Calls on one stream run in order and each leaves the workspace's
+        counters at zero, so they share one allocation (made on that
+        stream); ``fresh`` (debug buffers handed to the caller, or a debug
+        specialisation, which keeps its counters) allocates a new one."""
         if fresh:
             with torch.cuda.stream(stream):
-                return torch.empty((nbytes,), dtype=torch.uint8, device=device)
+                return torch.zeros((nbytes,), dtype=torch.uint8, device=device)
         key = (device.index if device.index is not None else 0, stream.cuda_stream)
         workspace = self._workspaces.get(key)
         if workspace is None or workspace.numel() < nbytes:
             if len(self._workspaces) >= 16:
                 self._workspaces.clear()
             with torch.cuda.stream(stream):
-                workspace = self._workspaces[key] = torch.empty((nbytes,), dtype=torch.uint8, device=device)
+                workspace = self._workspaces[key] = torch.zeros((nbytes,), dtype=torch.uint8, device=device)
         return workspace
 
     # ------------------------------------------------------------------
@@ -408,14 +409,20 @@ class CompiledProgram:
             workspace = None
             if plan.workspace_bytes:
                 workspace = self._workspace(torch, values.device, active, int(plan.workspace_bytes),
-                                            fresh=debug_buffers is not None)
+                                            fresh=debug_buffers is not None or self.spec.debug_visits)
             inputs = [values, offsets, out] + ([mask] if mask is not None else [])
             for tensor in inputs:
                 tensor.record_stream(active)
-            module.run_ref(plan_ref, values.data_ptr(), offsets.data_ptr(), out.data_ptr(),
-                           mask.data_ptr() if mask is not None else None,
-                           workspace.data_ptr() if workspace is not None else None, int(plan.workspace_bytes),
-                           active.cuda_stream)
+            try:
+                module.run_ref(plan_ref, values.data_ptr(), offsets.data_ptr(), out.data_ptr(),
+                               mask.data_ptr() if mask is not None else None,
+                               workspace.data_ptr() if workspace is not None else None, int(plan.workspace_bytes),
+                               active.cuda_stream)
+            except Exception:
+                # A launch that failed part way may leave the counters set:
+                # the next call on this stream gets a fresh zeroed workspace.
+                self._workspaces.pop((device, active.cuda_stream), None)
+                raise
             names += plan_names
             grids += plan_grids
             if debug_buffers is not None and workspace is not None:

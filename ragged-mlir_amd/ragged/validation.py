@@ -34,17 +34,19 @@ def _phase(op: str) -> str:
 
 
 def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> list[str]:
-    """Role names in launch order. The classified schedule runs init,
-    classify and one worker over the wave, block and split classes (plus the
-    split normalise pass of a softmax); with ``fused`` a softmax runs its
+    """Role names in launch order. The classified schedule runs classify
+    (which also initialises the per-segment state of the call) and one
+    worker over the wave, block and split classes (a softmax's worker also
+    normalises its split parts); with ``fused`` a softmax runs its
     register-resident worker, then a pass over the deferred chunks and the
-    wave class."""
+    wave class, after an init pass over its pair slots. The last kernel's
+    last workgroup returns the workspace's counters to zero."""
     phase = _phase(spec.op)
     if classes == ["block"] and spec.strategy == "naive":
         return [phase]
-    roles = ["init", "classify"]
     if fused:
-        return roles + ["fused_online", "deferred_online"]
+        return ["init", "classify", "fused_online", "deferred_online"]
+    roles = ["classify"]
     # One persistent worker drains every class; the reference's per-class
     # chains, split combine and (softmax) split normalisation run inside it.
     roles.append(f"worker_{phase}")
@@ -76,7 +78,8 @@ def workspace_layout(spec: ProgramSpec, classified: bool, fused: bool = False) -
     if spec.op == "softmax":
         workspace += [{"name": "partial_sums", "dtype": "f32", "shape": ["items", d]},
                       {"name": "max_stats", "dtype": "f32", "shape": ["B_split", d]},
-                      {"name": "sum_stats", "dtype": "f32", "shape": ["B_split", d]}]
+                      {"name": "sum_stats", "dtype": "f32", "shape": ["B_split", d]},
+                      {"name": "deferred", "dtype": "i64", "shape": ["items", "tiles"]}]
     if spec.debug_visits:
         workspace.append({"name": "visits", "dtype": "i32", "shape": ["B"]})
     return workspace

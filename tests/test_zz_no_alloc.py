@@ -60,7 +60,7 @@ def test_static_workspace_matches_rg_run(op, dtype, d, offsets_dtype, distributi
         out_rows = rows if op == "softmax" else b
         expected = torch.full((out_rows, d), float("nan"), dtype=tdtype, device=DEVICE)
         actual = torch.full_like(expected, float("nan"))
-        workspace = torch.empty((int(plan.workspace_bytes),), dtype=torch.uint8, device=DEVICE)
+        workspace = torch.zeros((int(plan.workspace_bytes),), dtype=torch.uint8, device=DEVICE)
         module.run(plan, x.data_ptr(), off.data_ptr(), expected.data_ptr(), None, workspace.data_ptr(),
                    int(plan.workspace_bytes), stream)
         module.run_static(plan, x.data_ptr(), off.data_ptr(), actual.data_ptr(), None, stream)
