@@ -10,13 +10,17 @@ one MI355X, inputs resident in HBM. Prints ONE JSON line:
 * ``roofline``: the dominant kernel's algorithmic bytes / its average
   duration (HIP events recorded around every launch inside the timed calls,
   on the stream the kernels run on), against the 8 TB/s HBM peak.
-* ``cpu_baseline``: the float64 NumPy oracle timed on this host on a bounded
-  sample of the same workload, scaled to µs per full call.
+* ``cpu_baseline``: the fastest of the CPU baselines timed on this host on a
+  bounded sample of the same workload (a prefix of segments holding 1/16 of
+  the rows), scaled to a full call: the float64 NumPy oracle on one thread
+  and the reference's PyTorch CPU baseline at one thread and at the
+  process's core share; every variant is listed beside it.
 
 Every measured configuration first passes the oracle (max bit-exact,
 sum/softmax within tolerance) on a sample of its segments.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--cold] [--all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--op OP] [--seeds S,..]
+                    [--cold [write|read]] [--all] [--details FILE] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -90,30 +94,116 @@ def oracle_gate(op, dtype, values_f32, offsets, out_device, torch, *, max_rows=6
     return stats
 
 
-def cpu_baseline(op, dtype, values_f32, offsets, *, target_seconds=15.0):
-    """Time the NumPy oracle (single thread) on a prefix of segments that holds
-    about 1/16 of the rows, scaled to µs per full call."""
-    import oracle
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo, as lscpu reports it)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_sample(offsets, fraction: int = 16):
+    """A prefix of segments holding about 1/``fraction`` of the rows:
+    (segments, sample offsets as i64, rows)."""
     lengths = np.diff(offsets.astype(np.int64))
     n = int(offsets[-1])
-    cut = int(np.searchsorted(np.cumsum(lengths), max(1, n // 16))) + 1
+    cut = int(np.searchsorted(np.cumsum(lengths), max(1, n // fraction))) + 1
     cut = min(cut, len(lengths))
     sample_offsets = offsets[:cut + 1].astype(np.int64)
-    rows = int(sample_offsets[-1])
+    return cut, sample_offsets, int(sample_offsets[-1])
+
+
+def _median_time(function, target_seconds: float) -> tuple[float, int]:
+    """Median wall time of ``function()`` over at least 5 runs (1 at least
+    when one run exceeds the budget), after one warm-up."""
+    function()
+    times, started = [], time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - started) < target_seconds or len(times) < 1:
+        t0 = time.perf_counter()
+        function()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline_oracle(op, dtype, values_f32, offsets, *, target_seconds=15.0):
+    """The float64 NumPy oracle (single thread) on a prefix of segments that
+    holds about 1/16 of the rows, scaled to µs per full call."""
+    import oracle
+    n = int(offsets[-1])
+    cut, sample_offsets, rows = cpu_sample(offsets)
     inputs = values_f32[:rows]
     if dtype == "bf16":
         inputs = oracle.quantize_bf16(inputs)
     function = {"sum": oracle.segment_sum, "max": oracle.segment_max, "softmax": oracle.segment_softmax}[op]
-    function(inputs, sample_offsets)   # warm-up
-    times, started = [], time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - started) < target_seconds or len(times) < 1:
-        t0 = time.perf_counter()
-        function(inputs, sample_offsets)
-        times.append(time.perf_counter() - t0)
-    per_call_us = float(np.median(times)) * 1e6 * (n / max(rows, 1))
-    return {"per_call_us": round(per_call_us, 1), "cores": 1, "kind": "port",
-            "sample": f"float64 NumPy oracle ({op}, one thread) on the first {cut} of {len(lengths)} segments "
-                      f"({rows} of {n} rows), median of {len(times)} runs after one warm-up, scaled by N/rows"}
+    seconds, runs = _median_time(lambda: function(inputs, sample_offsets), target_seconds)
+    per_call_us = seconds * 1e6 * (n / max(rows, 1))
+    return {"per_call_us": round(per_call_us, 1), "cores": 1, "kind": "port", "impl": "oracle-float64-numpy",
+            "sample": f"float64 NumPy oracle ({op}, one thread) on the first {cut} of {len(offsets) - 1} segments "
+                      f"({rows} of {n} rows), median of {runs} runs after one warm-up, scaled by N/rows"}
+
+
+def torch_cpu_reference(values, offsets, op):
+    """The reference's PyTorch baseline on the CPU (baselines/torch_reference.py:
+    12-16: torch.segment_reduce on f32, bf16 promoted and converted back), and
+    for softmax the same steps composed: segment max, repeat_interleave,
+    exp, segment sum, divide."""
+    import torch
+    work = values.float() if values.dtype == torch.bfloat16 else values
+    if op in ("sum", "max"):
+        return torch.segment_reduce(work, op, offsets=offsets, axis=0).to(values.dtype)
+    lengths = offsets[1:] - offsets[:-1]
+    maxima = torch.segment_reduce(work, "max", offsets=offsets, axis=0)
+    weights = torch.exp(work - torch.repeat_interleave(maxima, lengths, dim=0))
+    sums = torch.segment_reduce(weights, "sum", offsets=offsets, axis=0)
+    return (weights / torch.repeat_interleave(sums, lengths, dim=0)).to(values.dtype)
+
+
+def cpu_baseline_torch(op, dtype, values_f32, offsets, threads: int, *, target_seconds=15.0):
+    """torch_cpu_reference at ``threads`` intra-op threads on the same 1/16
+    prefix of segments, scaled to µs per full call."""
+    import torch
+    n = int(offsets[-1])
+    cut, sample_offsets, rows = cpu_sample(offsets)
+    values = torch.from_numpy(np.ascontiguousarray(values_f32[:rows]))
+    if dtype == "bf16":
+        values = values.to(torch.bfloat16)
+    off = torch.from_numpy(sample_offsets)
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        seconds, runs = _median_time(lambda: torch_cpu_reference(values, off, op), target_seconds)
+    finally:
+        torch.set_num_threads(previous)
+    per_call_us = seconds * 1e6 * (n / max(rows, 1))
+    return {"per_call_us": round(per_call_us, 1), "cores": threads, "kind": "port",
+            "impl": f"torch-{torch.__version__}-cpu",
+            "sample": f"torch CPU reference ({op}; baselines/torch_reference.py restated, softmax composed) at "
+                      f"{threads} threads on the first {cut} of {len(offsets) - 1} segments ({rows} of {n} rows), "
+                      f"median of {runs} runs after one warm-up, scaled by N/rows"}
+
+
+def cpu_baselines(op, dtype, values_f32, offsets, algorithmic_bytes: int) -> list[dict]:
+    """Every CPU baseline of one workload, each with its GB/s: the oracle on
+    one thread and the torch reference at one thread and at every core this
+    process may use (its affinity, capped by OMP_NUM_THREADS: a GPU box
+    shares its host between GPUs)."""
+    cores = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads_all = min(cores, share) if share > 0 else cores
+    variants = [cpu_baseline_oracle(op, dtype, values_f32, offsets)]
+    for threads in sorted({1, threads_all}):
+        variants.append(cpu_baseline_torch(op, dtype, values_f32, offsets, threads))
+    model = cpu_model()
+    for variant in variants:
+        variant["value"] = round(algorithmic_bytes / (variant["per_call_us"] * 1e-6) / 1e9, 3)
+        variant["unit"] = "GB/s"
+        variant["cpu_model"] = model
+        variant["affinity_cores"] = cores
+    return variants
 
 
 def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_wave: int, t_block: int,
@@ -181,6 +271,8 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
     max_len = workload.max_len if workload.pass_max_len else None
     results = []
     for op in workload.ops:
+        if args.op and op != args.op:
+            continue
         program = Compiler().compile(ProgramSpec(op, workload.dtype, workload.d, workload.offsets_dtype), cache)
         rows = workload.n if op == "softmax" else workload.b
         out = torch.empty((rows, workload.d), dtype=tdtype, device=device)
@@ -203,13 +295,21 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
             chosen = program.naive if report.selected == "naive" else program
             module = _modules[(0, chosen._digest)]
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            flush = torch.empty((1 << 30,), dtype=torch.uint8, device=device) if args.cold else None
+            # Cold cache: before every call, overwrite (write flush) or read
+            # (read flush) 1 GiB, 4x the 256 MiB Infinity Cache plus L2.
+            flush = torch.empty((1 << 28,), dtype=torch.float32, device=device).fill_(1) if args.cold else None
+
+            def evict():
+                if args.cold == "read":
+                    flush.sum()
+                else:
+                    flush.fill_(1)
 
             def timed_calls() -> float:
                 if args.cold:
                     total_ms, host = 0.0, []
                     for _ in range(args.steps):
-                        flush.fill_(1)
+                        evict()
                         start.record()
                         t_host = time.perf_counter()
                         program.run(x, off, out, select=select, max_len=max_len)
@@ -253,7 +353,7 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
                 "us_per_call": round(ms * 1e3, 2), "gbps": round(gbps, 1), "pct_of_peak": round(100 * gbps / PEAK_GBPS, 2),
                 "gpu_us_per_call": round(gpu_ms * 1e3, 2), "host_us_per_run": host_us[0] if host_us else None,
                 "algorithmic_bytes": total_bytes, "kernels": kernels,
-                "dominant": dominant, "cold": bool(args.cold), "oracle": stats,
+                "dominant": dominant, "cold": args.cold or False, "seed": seed, "oracle": stats,
                 "n": workload.n, "b": workload.b, "d": workload.d, "dtype": workload.dtype,
                 "offsets_dtype": workload.offsets_dtype, "max_len": workload.max_len,
                 "kernel_names": list(report.kernel_names), "grids": [list(g) for g in report.grids]})
@@ -303,7 +403,13 @@ def main(argv=None) -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--config", default="c5", choices=["c1", "c2", "c3", "c4", "c5"])
-    parser.add_argument("--cold", action="store_true", help="flush 1 GiB (> MALL + L2) before every call")
+    parser.add_argument("--cold", nargs="?", const="write", choices=["write", "read"],
+                        help="flush 1 GiB (> MALL + L2) before every call, by overwriting it (write, the "
+                             "default) or by reading it (read)")
+    parser.add_argument("--seeds", help="comma-separated seeds (default: 711, 712, 713 for c1, else 711); "
+                                        "the line reports the median seed")
+    parser.add_argument("--op", choices=["sum", "max", "softmax"],
+                        help="measure only this op of the workload (c2 holds sum and max)")
     parser.add_argument("--all", action="store_true", help="also measure forced classified and naive schedules")
     parser.add_argument("--details", type=Path, help="write every measured record as JSON to this file")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -322,16 +428,28 @@ def main(argv=None) -> int:
     if args.copy_probe:
         return copy_probe(torch, args.copy_probe, args.steps)
     from ragged import ArtifactCache
+    seeds = ([int(x) for x in args.seeds.split(",")] if args.seeds
+             else [711, 712, 713] if args.config == "c1" else [711])
     with tempfile.TemporaryDirectory(prefix="ragged-bench-") as directory:
         cache = ArtifactCache(directory)
-        records, workload = run_config(args.config, args, torch, cache)
-        headline = next(r for r in records if r["select"] == "auto")
-        baseline = None
+        records, autos = [], []
+        for seed in seeds:
+            seed_records, workload = run_config(args.config, args, torch, cache, seed=seed)
+            records += seed_records
+            autos.append((next(r for r in seed_records if r["select"] == "auto"), workload))
+        # The line reports the seed of median time (the only one for one seed).
+        autos.sort(key=lambda pair: pair[0]["us_per_call"])
+        headline, workload = autos[len(autos) // 2]
+        baseline, variants = None, []
         if not args.no_cpu:
-            sample = cpu_baseline(headline["op"], workload.dtype, workload.values, workload.offsets)
-            baseline = {"value": round(headline["algorithmic_bytes"] / (sample["per_call_us"] * 1e-6) / 1e9, 3),
-                        "unit": "GB/s", **sample}
-            log(f"[bench] cpu baseline: {baseline}")
+            variants = cpu_baselines(headline["op"], workload.dtype, workload.values, workload.offsets,
+                                     headline["algorithmic_bytes"])
+            best = max(variants, key=lambda v: v["value"])
+            baseline = {key: best[key] for key in ("value", "unit", "cores", "kind", "sample", "per_call_us",
+                                                   "impl", "cpu_model", "affinity_cores")}
+            baseline["variants"] = [{key: v[key] for key in ("impl", "cores", "value", "per_call_us")}
+                                    for v in variants]
+            log(f"[bench] cpu baselines: {json.dumps(variants)}")
     dominant = headline["dominant"]
     kernel = headline["kernels"].get(dominant, {})
     measured = measured_traffic(headline["workload"], dominant)
@@ -349,13 +467,15 @@ def main(argv=None) -> int:
         "dtype": headline["dtype"], "data": "synthetic (seeded NumPy generators, resident in HBM)",
         "config": {"workload": headline["workload"], "op": headline["op"], "n": headline["n"], "b": headline["b"],
                    "d": headline["d"], "offsets": headline["offsets_dtype"], "max_len": headline["max_len"],
-                   "schedule": headline["selected"], "cache": "cold" if args.cold else "warm",
-                   "parallelism": "single GPU"},
+                   "schedule": headline["selected"],
+                   "cache": f"cold ({args.cold} flush)" if args.cold else "warm",
+                   "seeds": seeds, "seed": headline["seed"], "parallelism": "single GPU"},
         "roofline": roofline, "cpu_baseline": baseline,
     }
     if args.details:
         args.details.parent.mkdir(parents=True, exist_ok=True)
-        args.details.write_text(json.dumps({"line": line, "records": records}, indent=1) + "\n")
+        args.details.write_text(json.dumps({"line": line, "records": records, "cpu_baselines": variants},
+                                           indent=1) + "\n")
     print(json.dumps(line), flush=True)
     return 0
 

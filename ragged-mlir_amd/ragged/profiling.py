@@ -10,7 +10,13 @@ summarises Nsight Compute metrics) for rocprofv3 output on gfx950:
   reports (one per TCC channel on some ROCm versions);
 * ``traffic``: FETCH_SIZE and WRITE_SIZE runs of a workload, each scaled by
   the factor the same counter reads for a plain copy of known size
-  (``bench.py --copy-probe``), into HBM bytes per launch.
+  (``bench.py --copy-probe``), into HBM bytes per launch;
+* ``resources``: per kernel, the VGPR / AGPR / SGPR / LDS / scratch figures
+  and grid the kernel trace records for its dispatches;
+* ``report``: one workload's markdown table per kernel from a stats run, the
+  FETCH_SIZE / WRITE_SIZE runs and an occupancy run (OccupancyPercent,
+  MeanOccupancyPerCU, VALUBusy, MemUnitStalled) plus the algorithmic bytes a
+  ``bench.py --details`` file records per kernel role.
 
 Both output formats are read: the SQLite database rocprofv3 writes by
 default (``*_results.db``, views ``kernels`` and ``counters_collection``) and
@@ -129,6 +135,87 @@ def traffic(fetch_csv: Path, write_csv: Path, pattern: str, factor: dict[str, fl
             "bytes": read_bytes + write_bytes}
 
 
+RESOURCE_COLUMNS = ("vgpr_count", "accum_vgpr_count", "sgpr_count", "lds_size", "static_lds_size", "scratch_size",
+                    "static_scratch_size", "grid_x", "workgroup_x")
+
+
+def kernel_resources(path: Path) -> dict[str, dict[str, float]]:
+    """Per kernel (database only): dispatches and the mean of each
+    RESOURCE_COLUMNS figure over them."""
+    columns = ", ".join(RESOURCE_COLUMNS)
+    out: dict[str, dict[str, float]] = {}
+    for row in _query(path, f"select name, {columns} from kernels"):
+        entry = out.setdefault(short_name(row[0]), {"dispatches": 0, **{c: 0.0 for c in RESOURCE_COLUMNS}})
+        entry["dispatches"] += 1
+        for column, value in zip(RESOURCE_COLUMNS, row[1:]):
+            entry[column] += float(value or 0)
+    for entry in out.values():
+        for column in RESOURCE_COLUMNS:
+            entry[column] /= entry["dispatches"]
+    return out
+
+
+# Kernel-name patterns of the library's launch roles (bench.py --details keys).
+ROLE_PATTERNS = {"init": r"k_init\b", "classify": r"k_classify", "worker": r"k_worker",
+                 "fused": r"k_softmax_fused", "deferred": r"k_softmax_deferred", "naive": r"k_naive"}
+# rocprofv3 reports vgpr_count as (descriptor granules) x 4; gfx950 wave64
+# allocates VGPRs in granules of 8 (compiler remarks: 44 -> 24, 128 -> 64).
+VGPR_DECODE = 2
+OCCUPANCY_COUNTERS = ("OccupancyPercent", "MeanOccupancyPerCU", "VALUBusy", "MemUnitStalled")
+
+
+def report(stats_db: Path, fetch_db: Path, write_db: Path, occupancy_db: Path, factor: dict[str, float],
+           roles: dict[str, dict], title: str, peak_gbps: float = 8000.0) -> list[str]:
+    """Markdown lines: per launched role, the rocprofv3 average duration,
+    algorithmic bytes and GB/s, HBM bytes (counters scaled by the copy
+    factor) and their ratio to the algorithmic bytes, occupancy and the
+    kernel's register / LDS / scratch use."""
+    stats = kernel_stats(stats_db)
+    resources = kernel_resources(stats_db)
+    fetch = counter_per_dispatch(fetch_db, "FETCH_SIZE")
+    write = counter_per_dispatch(write_db, "WRITE_SIZE")
+    occupancy = {counter: counter_per_dispatch(occupancy_db, counter) for counter in OCCUPANCY_COUNTERS}
+    lines = [f"### {title}", "",
+             "| role | kernel | calls | avg µs | algorithmic MB | GB/s (% of peak) | HBM read MB | HBM write MB | "
+             "HBM / algorithmic | occupancy % | waves/CU | VALU busy % | mem stalled % | VGPR alloc | AGPR alloc | "
+             "SGPR | LDS B | scratch B/lane | grid |",
+             "|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for role, info in roles.items():
+        pattern = ROLE_PATTERNS.get(role)
+        if pattern is None:
+            continue
+        try:
+            name, stat = _match(stats, pattern)
+        except KeyError:
+            continue
+        avg_us = stat["avg_ns"] / 1e3
+        algorithmic = float(info.get("bytes") or 0)
+        gbps = algorithmic / (avg_us * 1e-6) / 1e9 if avg_us > 0 else 0.0
+
+        def mean(table, default=float("nan")):
+            try:
+                return _match(table, pattern)[1]["mean"]
+            except KeyError:
+                return default
+
+        read_bytes = mean(fetch) * factor["fetch_bytes_per_unit"]
+        write_bytes = mean(write) * factor["write_bytes_per_unit"]
+        ratio = (read_bytes + write_bytes) / algorithmic if algorithmic else float("nan")
+        res = _match(resources, pattern)[1]
+        occ = {counter: mean(table) for counter, table in occupancy.items()}
+        lines.append(
+            f"| {role} | `{name}` | {stat['calls']} | {avg_us:.2f} | {algorithmic / 1e6:.2f} | "
+            f"{gbps:.0f} ({100 * gbps / peak_gbps:.1f}%) | {read_bytes / 1e6:.2f} | {write_bytes / 1e6:.2f} | "
+            f"{ratio:.3f} | {occ['OccupancyPercent']:.1f} | {occ['MeanOccupancyPerCU']:.1f} | "
+            f"{occ['VALUBusy']:.1f} | {occ['MemUnitStalled']:.1f} | {VGPR_DECODE * res['vgpr_count']:.0f} | "
+            f"{VGPR_DECODE * res['accum_vgpr_count']:.0f} | {res['sgpr_count']:.0f} | {res['lds_size']:.0f} | "
+            f"{res['scratch_size']:.0f} | {res['grid_x'] / max(res['workgroup_x'], 1):.0f} |")
+    lines += ["", f"VGPR / AGPR alloc: rocprofv3's `vgpr_count` x {VGPR_DECODE} (it decodes the kernel "
+                  "descriptor's register granule as 4; gfx950 wave64 allocates 8 per granule, which the compiler's "
+                  "resource remarks confirm). Occupancy counters come from a separate --pmc run."]
+    return lines
+
+
 def stats_table(stats: dict[str, dict[str, float]], limit: int = 12) -> Iterable[str]:
     yield "| kernel | calls | avg µs | total µs | % |"
     yield "|---|---:|---:|---:|---:|"
@@ -158,7 +245,31 @@ def main(argv: list[str] | None = None) -> int:
     t.add_argument("--library", type=Path, help="the libragged_hip.so that was profiled (its sha256 is recorded)")
     t.add_argument("--command", action="append", default=[], help="a command that produced the inputs (repeat)")
     t.add_argument("--out", type=Path, help="also write the result as JSON here")
+    r = sub.add_parser("resources", help="VGPR/AGPR/SGPR/LDS/scratch per kernel of a kernel-trace database")
+    r.add_argument("db", type=Path)
+    m = sub.add_parser("report", help="markdown per-kernel table of one workload")
+    m.add_argument("--stats", type=Path, required=True, help="--kernel-trace --stats database")
+    m.add_argument("--fetch", type=Path, required=True)
+    m.add_argument("--write", type=Path, required=True)
+    m.add_argument("--occupancy", type=Path, required=True, help="--pmc " + " ".join(OCCUPANCY_COUNTERS))
+    m.add_argument("--copy-fetch", type=Path, required=True)
+    m.add_argument("--copy-write", type=Path, required=True)
+    m.add_argument("--copy-bytes", type=int, required=True)
+    m.add_argument("--copy-kernel", default="copy|elementwise", help="regex of the copy kernel")
+    m.add_argument("--details", type=Path, required=True, help="bench.py --details output")
+    m.add_argument("--op", help="the op of the details record to use (default: the first)")
+    m.add_argument("--title", required=True)
     args = parser.parse_args(argv)
+    if args.command == "resources":
+        print(json.dumps(kernel_resources(args.db), indent=1))
+        return 0
+    if args.command == "report":
+        factor = copy_factor(args.copy_fetch, args.copy_write, args.copy_bytes, args.copy_kernel)
+        records = json.loads(args.details.read_text())["records"]
+        record = next(r for r in records if r["select"] == "auto" and (args.op is None or r["op"] == args.op))
+        print("\n".join(report(args.stats, args.fetch, args.write, args.occupancy, factor, record["kernels"],
+                               args.title)))
+        return 0
     if args.command == "stats":
         table = kernel_stats(args.csv)
         print(json.dumps(table, indent=1) if args.json else "\n".join(stats_table(table)))
