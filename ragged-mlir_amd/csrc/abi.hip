@@ -526,6 +526,11 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
         !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE]) || !mul_ok(item_bytes, 2, &sizes[RG_BUF_PAIRS]) ||
         !mul_ok(stat_bytes, 2, &sizes[RG_BUF_FINAL_PAIRS]))
       return fail(RG_E_INVALID, "fused softmax workspace bytes overflow");
+    // A merge folds a segment's pairs through one buffer resource, whose
+    // offsets are 32-bit: the whole pair table stays below 2 GiB.
+    if (sizes[RG_BUF_PAIRS] > INT32_MAX)
+      return fail(RG_E_INVALID, "register-resident softmax: the pair table of this plan exceeds 2 GiB "
+                                "(items_cap x feature_dim x 8 bytes); run this input through the naive program");
   }
   plan->fused = module->fused ? 1 : 0;
   if (spec.debug_visits && !mul_ok(b, 4, &sizes[RG_BUF_VISITS])) return fail(RG_E_INVALID, "visits bytes overflow");

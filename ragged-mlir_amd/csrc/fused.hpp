@@ -238,17 +238,31 @@ __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F7
 // segment of one group publishes it from the group fold.
 constexpr int kBatch = 8;            // pair loads in flight per thread
 
-// One thread's fold of slots base[0], base[stride * d], ... (count of them)
-// of feature f, in slot order, kBatch loads at a time; ok turns false if a
-// slot still holds the sentinel.
-__device__ __forceinline__ State<OP_SOFTMAX> fold_range(const uint64_t* base, int64_t count, int64_t stride, int d,
-                                                        int64_t f, bool& ok) {
+// Pair loads of a fold go through one wave-uniform resource over the slots
+// it reads: the slot's byte offset is uniform (an SGPR), the feature's is
+// per lane, so kBatch loads in flight hold only their results in VGPRs (64-bit
+// per-lane addresses would take as many again, and the fused kernel, which
+// holds its rows meanwhile, would spill). The cache policy is sc1, the
+// agent-scope coherence of a relaxed atomic load on gfx950; every poll is
+// separated from the next by a barrier (a fence), so the compiler cannot
+// reuse an earlier load's value.
+constexpr int kPairAux = 16;
+
+__device__ __forceinline__ uint64_t load_pair_at(Rsrc r, int voffset, int soffset) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voffset, soffset, kPairAux);
+  return ((uint64_t)v[1] << 32) | v[0];
+}
+
+// One thread's fold of `count` slots, slot_bytes apart, starting voff bytes
+// into resource r, in slot order, kBatch loads at a time; ok turns false if
+// a slot still holds the sentinel.
+__device__ __forceinline__ State<OP_SOFTMAX> fold_range(Rsrc r, int voff, int count, int slot_bytes, bool& ok) {
   State<OP_SOFTMAX> acc;
   acc.init();
-  for (int64_t i0 = 0; i0 < count; i0 += kBatch) {
+  for (int i0 = 0; i0 < count; i0 += kBatch) {
     uint64_t v[kBatch];
 #pragma unroll
-    for (int j = 0; j < kBatch; ++j) v[j] = i0 + j < count ? load_pair(base + (i0 + j) * stride * d + f) : 0;
+    for (int j = 0; j < kBatch; ++j) v[j] = i0 + j < count ? load_pair_at(r, voff, (i0 + j) * slot_bytes) : 0;
 #pragma unroll
     for (int j = 0; j < kBatch; ++j) {
       if (i0 + j < count) {
@@ -269,15 +283,19 @@ __device__ __forceinline__ State<OP_SOFTMAX> fold_range(const uint64_t* base, in
 // the R range results are folded in range order through `stage` (R * d
 // pairs). The association depends only on (count, d): deterministic. True,
 // after a barrier, when no slot held the sentinel.
+// A fold reads at most (count - 1) * stride + 1 slots of d pairs from base:
+// a segment's chunks or groups, far below 2^31 bytes (the plan checks it).
 __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, int64_t stride, int d, float* lds_m,
                                            float* lds_s, uint64_t* stage) {
   const int t = threadIdx.x;
   int r = 1;
   while (2 * r * d <= kBlock && 2 * r <= count) r *= 2;
   bool ok = true;
+  const int slot_bytes = (int)(stride * d * 8);
+  const Rsrc pairs = make_rsrc(base, ((count - 1) * stride * d + d) * 8);
   if (r == 1) {
     for (int f = t; f < d; f += kBlock) {
-      const State<OP_SOFTMAX> st = fold_range(base, count, stride, d, f, ok);
+      const State<OP_SOFTMAX> st = fold_range(pairs, f * 8, (int)count, slot_bytes, ok);
       lds_m[f] = st.m;
       lds_s[f] = st.s;
     }
@@ -285,8 +303,8 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
   }
   if (t < r * d) {
     const int part = t / d, f = t - part * d;
-    const int64_t lo = count * part / r, hi = count * (part + 1) / r;
-    const State<OP_SOFTMAX> st = fold_range(base + lo * stride * d, hi - lo, stride, d, f, ok);
+    const int lo = (int)(count * part / r), hi = (int)(count * (part + 1) / r);
+    const State<OP_SOFTMAX> st = fold_range(pairs, lo * slot_bytes + f * 8, hi - lo, slot_bytes, ok);
     stage[t] = pack_pair(st.m, st.s);
   }
   const bool all = !block_any(!ok);
