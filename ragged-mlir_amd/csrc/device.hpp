@@ -92,6 +92,23 @@ __device__ __forceinline__ float exp_out(float x) {
   if constexpr (std::is_same<T, float>::value) return exp_split(x);
   else return __expf(x);
 }
+// exp(x - ref) over rows of type T that share a column reference ref: bf16
+// rows as 2^(x log2(e) - ref log2(e)), one FMA into v_exp_f32 with
+// shift = -ref log2(e) computed once per column (the error of the rounded
+// shift, below 2^-24 |ref| log2(e) in the exponent, is far below a bf16
+// ulp); f32 rows through exp_split(x - ref). ±inf and NaN follow x - ref:
+// inf - inf and NaN give NaN, x - inf gives 0.
+template <class T>
+struct ExpShift {
+  float ref = 0.f, shift = 0.f;
+  ExpShift() = default;
+  __device__ explicit ExpShift(float r) : ref(r), shift(-r * kLog2eHi) {}
+  __device__ float operator()(float x) const {
+    if constexpr (std::is_same<T, float>::value) return exp_split(x - ref);
+    else return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2eHi, shift));
+  }
+};
+
 // e = exp(x - m) in [0, 1] of bf16 rows held in registers between the two
 // passes of the register-resident softmax, as 16-bit unsigned normalised
 // integers (v_cvt_pknorm_u16_f32, round to nearest): an absolute error of at

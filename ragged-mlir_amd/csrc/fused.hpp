@@ -283,11 +283,21 @@ __device__ __forceinline__ State<OP_SOFTMAX> fold_range(Rsrc r, int voff, int co
 // the R range results are folded in range order through `stage` (R * d
 // pairs). The association depends only on (count, d): deterministic. True,
 // after a barrier, when no slot held the sentinel.
+// The thread index through an opaque copy: values derived from it inside a
+// persistent kernel's loop are recomputed where they are used (a few
+// integer instructions) instead of being hoisted before the loop and kept
+// in registers the held rows need, or spilled.
+__device__ __forceinline__ int local_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // A fold reads at most (count - 1) * stride + 1 slots of d pairs from base:
 // a segment's chunks or groups, far below 2^31 bytes (the plan checks it).
 __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, int64_t stride, int d, float* lds_m,
                                            float* lds_s, uint64_t* stage) {
-  const int t = threadIdx.x;
+  const int t = local_tid();
   int r = 1;
   while (2 * r * d <= kBlock && 2 * r <= count) r *= 2;
   bool ok = true;
@@ -345,7 +355,7 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
 // its own column max from its rows, not from its pair slot.
 __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t k, int* flag_s,
                            float* lds_m, float* lds_s, uint64_t* stage) {
-  const int t = threadIdx.x;
+  const int t = local_tid();
   const int d = p.d;
   const int64_t group = (slot - first) / kGroup;
   const int64_t gfirst = first + group * kGroup;
@@ -538,10 +548,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     }
     // 2. e = exp(x - m) in place, column sums. A column of only -inf has no
     //    mass: its reference is taken as 0 so that e = 0, not NaN.
-    float ref[VEC], sum[VEC];
+    float sum[VEC];
+    ExpShift<T> ex[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      ref[v] = m[v] == neg_inf() ? 0.f : m[v];
+      ex[v] = ExpShift<T>(m[v] == neg_inf() ? 0.f : m[v]);
       sum[v] = 0.f;
     }
 #pragma unroll
@@ -550,7 +561,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       float e[VEC];
 #pragma unroll
       for (int v = 0; v < VEC; ++v) {
-        e[v] = exp_out<T>(Reg::get(data[i], v) - ref[v]);
+        e[v] = ex[v](Reg::get(data[i], v));
         sum[v] += e[v];
       }
       if constexpr (kUnorm) {
@@ -590,7 +601,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       const int64_t idx = index_of(ticket);
       const int64_t first = idx - it.c;
       const int64_t parts = it.parts;
-      for (int f = t; f < d; f += kBlock) store_pair(p.pairs + idx * d + f, own_m[f], own_s[f]);
+      for (int f = local_tid(); f < d; f += kBlock) store_pair(p.pairs + idx * d + f, own_m[f], own_s[f]);
       const bool direct = parts <= kDirect;
       if (!direct) tree_merge(p, idx, first, parts, it.k, &flag_s, lds, lds_s, stage);
       if (!may_wait) {
@@ -672,7 +683,7 @@ __device__ __forceinline__ void renormalize_rows(const Params& p, const RowGeo& 
     load_input<T, VEC, MASK>(p, r * p.d + g.feature, x);
 #pragma unroll
     for (int v = 0; v < VEC; ++v) {
-      float e = exp_out<T>(x[v] - ref[v]);
+      float e = ExpShift<T>(ref[v])(x[v]);
       if (unorm) e = unorm_lo(pack_unorm(e, 0.f));
       x[v] = e * factor[v];
     }
