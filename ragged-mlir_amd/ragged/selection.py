@@ -9,9 +9,9 @@ families are the reference's {reduce, softmax} plus ``softmax_fused``: a
 softmax whose classified schedule is the register-resident worker pays a
 per-segment cost the streaming worker does not, so it gets its own fit.
 
-The terms are re-derived for MI355X (model version 4, eight terms, µs):
+The terms are re-derived for MI355X (model version 5, nine terms, µs):
 
-    t = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall
+    t = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall + c8*W*A
 
 W = MiB the call moves (rows read; rows written for softmax, B result rows
 for sum/max); S = L*D*element_bytes / 2^20, the MiB the one workgroup that
@@ -22,7 +22,10 @@ pays most per segment there) and R = row KiB (D*element_bytes / 1024);
 X_l2 / X_mall = MiB of the working set (input rows plus output rows) beyond
 the total L2 (8 XCDs x 4 MiB) and beyond the 256 MiB Infinity Cache. The
 reference's single "beyond the 72 MiB L2" term becomes two because MI355X
-has two cache levels of very different size in front of HBM.
+has two cache levels of very different size in front of HBM. A = 16 /
+access bytes - 1, where a lane's access is the mapping's vector (16 bytes
+for D dividing or divided by the 16-byte vector, else the largest power of
+two of elements dividing D): the extra cost per MiB of narrower accesses.
 """
 from __future__ import annotations
 
@@ -37,8 +40,8 @@ from .errors import CacheMismatch
 MODEL_PATH = Path(__file__).with_name("cost_model.json")
 SCHEDULES = ("classified", "naive")
 FAMILIES = ("reduce", "softmax", "softmax_fused")
-TERMS = 8
-VERSION = 4
+TERMS = 9
+VERSION = 5
 
 
 def family(op: str, fused: bool = False) -> str:
@@ -49,14 +52,25 @@ def family(op: str, fused: bool = False) -> str:
 
 def features(n: int, b: int, d: int, max_len: int, element_bytes: int = 4, op: str = "sum",
              l2_mib: float = 32.0, mall_mib: float = 256.0, flat: bool = False) -> tuple[float, ...]:
-    """The eight prediction terms for one call."""
+    """The nine prediction terms for one call."""
     row = d * element_bytes
     rows = n * row / 2**20
     output_rows = n if op == "softmax" else b
     moved = rows + output_rows * row / 2**20
     segments = b / 1000.0
     return (1.0, moved, max_len * row / 2**20, segments, segments if flat else 0.0, segments * row / 1024,
-            max(0.0, moved - l2_mib), max(0.0, moved - mall_mib))
+            max(0.0, moved - l2_mib), max(0.0, moved - mall_mib), moved * (16 / access_bytes(d, element_bytes) - 1))
+
+
+def access_bytes(d: int, element_bytes: int) -> int:
+    """Bytes of one lane's access in the default geometry (Optimizations.geometry)."""
+    widest = 16 // element_bytes
+    if d < widest and widest % d == 0:
+        return 16
+    vec = 1
+    while vec * 2 <= widest and d % (vec * 2) == 0:
+        vec *= 2
+    return vec * element_bytes
 
 
 @dataclass(frozen=True)

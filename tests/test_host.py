@@ -17,7 +17,8 @@ import pytest
 from ragged import ProgramSpec
 from ragged import native
 from ragged.errors import RuntimeUnavailable, ValidationError
-from ragged.selection import features
+from ragged.optimizations import Optimizations
+from ragged.selection import access_bytes, features
 from ragged.validation import CONDITIONS, I64_MAX, raise_for_status
 from ragged.workloads import describe, make_lengths, offsets_from_lengths, reference_values, sha256
 
@@ -156,13 +157,22 @@ def test_status_decoding_known_answers():
 def test_cost_model_features_known_answer():
     # N = 2^20 rows, B = 1024, D = 4 f32 (16-byte rows), L = 2^14: W = 16 MiB of rows read + 1024
     # result rows = 16.015625 MiB; S = 2^14*16/2^20 = 0.25 MiB; B/1000 = 1.024; row mapping (F = 0);
-    # R*B/1000 = 1.024 * 16/1024; the working set is under the 32 MiB L2.
+    # R*B/1000 = 1.024 * 16/1024; the working set is under the 32 MiB L2; 16-byte accesses (A = 0).
     assert features(2**20, 1024, 4, 2**14, 4, "sum") == (1.0, 16.015625, 0.25, 1.024, 0.0, 1.024 * 16 / 1024,
-                                                          0.0, 0.0)
+                                                          0.0, 0.0, 0.0)
     assert features(2**20, 1024, 4, 2**14, 4, "sum", flat=True)[4] == 1.024
     # Softmax writes N rows: 128 MiB of rows at D=32 f32 -> 256 MiB moved.
     f = features(2**20, 1024, 32, 2**14, 4, "softmax")
-    assert f[1] == 256.0 and f[6] == pytest.approx(256.0 - 32.0) and f[7] == 0.0
+    assert f[1] == 256.0 and f[6] == pytest.approx(256.0 - 32.0) and f[7] == 0.0 and f[8] == 0.0
+    # Access width: D=3 f32 reads 4-byte elements (A = 3), D=6 f32 8 bytes (A = 1), D=10 bf16 4 bytes
+    # (A = 3), D=2 f32 and D=4 bf16 the flat 16-byte vector (A = 0).
+    assert [access_bytes(d, e) for d, e in ((3, 4), (6, 4), (10, 2), (2, 4), (4, 2), (12, 2))] == [4, 8, 4, 16, 16, 8]
+    assert features(1000, 10, 3, 100, 4, "sum")[8] == pytest.approx(3 * features(1000, 10, 3, 100, 4, "sum")[1])
+    # The same width as the geometry the programs are built with.
+    for dtype, element in (("f32", 4), ("bf16", 2)):
+        for d in range(1, 300):
+            _, vec, mapping = Optimizations().geometry(d, dtype)
+            assert access_bytes(d, element) == (16 if mapping == "flat" else vec * element), (d, dtype)
 
 
 def test_product_fails_loudly_without_the_library(monkeypatch, tmp_path):
