@@ -364,17 +364,65 @@ __device__ __forceinline__ void init_all(State<OP> (&st)[V]) {
 // ---------------------------------------------------------------------------
 // Cross-lane combination.
 
-template <int OP>
-__device__ __forceinline__ State<OP> shfl_xor(const State<OP>& a, int mask) {
+// The value of lane (lane ^ MASK), MASK a power of two below 64, through
+// gfx950's lane-crossing operations instead of ds_bpermute (an LDS-crossbar
+// access with a per-lane address): DPP quad permutes for 1 and 2, a
+// ds_swizzle bit-mode exchange for 4, DPP row_ror:8 for 8 (a rotation by
+// half a 16-lane row is the xor), and v_permlane16_swap / v_permlane32_swap
+// for 16 and 32 (each swap returns both halves; a lane takes its partner's).
+// Every mask is the exact xor exchange, so reductions built on it associate
+// as an xor butterfly and every lane of a group ends with the same bits.
+template <int MASK>
+__device__ __forceinline__ float xor_lane(float v) {
+  static_assert(MASK > 0 && MASK < 64 && (MASK & (MASK - 1)) == 0, "mask must be a power of two below 64");
+  const int x = __float_as_int(v);
+  if constexpr (MASK == 1) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+  if constexpr (MASK == 2) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+  if constexpr (MASK == 4) return __int_as_float(__builtin_amdgcn_ds_swizzle(x, (4 << 10) | 0x1F));   // and 0x1F, xor 4
+  if constexpr (MASK == 8) return __int_as_float(__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+  if constexpr (MASK == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return __int_as_float((int)((threadIdx.x & 16) ? r[0] : r[1]));
+  }
+  if constexpr (MASK == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return __int_as_float((int)((threadIdx.x & 32) ? r[0] : r[1]));
+  }
+}
+
+// Butterfly over the lanes whose index agrees modulo `stride` (a uniform
+// power of two): fn(mask-level callable) is applied at every compile-time
+// mask from stride to 32, each step behind one uniform branch.
+template <class Step>
+__device__ __forceinline__ void xor_butterfly(int stride, Step&& step) {
+  if (stride <= 1) step(std::integral_constant<int, 1>{});
+  if (stride <= 2) step(std::integral_constant<int, 2>{});
+  if (stride <= 4) step(std::integral_constant<int, 4>{});
+  if (stride <= 8) step(std::integral_constant<int, 8>{});
+  if (stride <= 16) step(std::integral_constant<int, 16>{});
+  if (stride <= 32) step(std::integral_constant<int, 32>{});
+}
+
+// Lane `src`'s value (src wave-uniform) in every lane, through the scalar
+// unit (v_readlane) instead of an LDS-crossbar broadcast.
+__device__ __forceinline__ int64_t lane_value(int64_t v, int src) {
+  const uint32_t lo = __builtin_amdgcn_readlane((int)(uint32_t)(uint64_t)v, src);
+  const uint32_t hi = __builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), src);
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int lane_value(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
+
+template <int MASK, int OP>
+__device__ __forceinline__ State<OP> shfl_xor(const State<OP>& a) {
   State<OP> r;
   if constexpr (OP == OP_SUM) {
-    r.s = __shfl_xor(a.s, mask, kWave);
+    r.s = xor_lane<MASK>(a.s);
     r.c = 0.f;
   } else if constexpr (OP == OP_MAX) {
-    r.m = __shfl_xor(a.m, mask, kWave);
+    r.m = xor_lane<MASK>(a.m);
   } else {
-    r.m = __shfl_xor(a.m, mask, kWave);
-    r.s = __shfl_xor(a.s, mask, kWave);
+    r.m = xor_lane<MASK>(a.m);
+    r.s = xor_lane<MASK>(a.s);
   }
   return r;
 }
@@ -383,10 +431,10 @@ __device__ __forceinline__ State<OP> shfl_xor(const State<OP>& a, int mask) {
 // afterwards every lane holds the combination over its residue class.
 template <int OP, int V>
 __device__ __forceinline__ void wave_reduce_stride(State<OP> (&st)[V], int stride) {
-  for (int mask = stride; mask < kWave; mask <<= 1) {
+  xor_butterfly(stride, [&](auto mask) {
 #pragma unroll
-    for (int v = 0; v < V; ++v) st[v].merge(shfl_xor<OP>(st[v], mask));
-  }
+    for (int v = 0; v < V; ++v) st[v].merge(shfl_xor<decltype(mask)::value, OP>(st[v]));
+  });
 }
 
 template <int OP> struct Slots { static constexpr int kCount = OP == OP_SOFTMAX ? 2 : 1; };

@@ -167,10 +167,10 @@ template <bool MAX, int VEC>
 __device__ __forceinline__ void block_allreduce(float (&v)[VEC], int lpr, int feat_lane, float* lds) {
   const int t = threadIdx.x, lane = t & (kWave - 1), w = t / kWave;
   auto combine = [](float a, float b) { return MAX ? fmax_nan(a, b) : a + b; };
-  for (int mask = lpr; mask < kWave; mask <<= 1) {
+  xor_butterfly(lpr, [&](auto mask) {
 #pragma unroll
-    for (int i = 0; i < VEC; ++i) v[i] = combine(v[i], __shfl_xor(v[i], mask, kWave));
-  }
+    for (int i = 0; i < VEC; ++i) v[i] = combine(v[i], xor_lane<decltype(mask)::value>(v[i]));
+  });
   const int rep = lpr < kWave ? lpr : kWave;
   if (lane < rep) {
     float* slot = lds + (w * kWave + lane) * VEC;

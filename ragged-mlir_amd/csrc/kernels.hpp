@@ -593,13 +593,13 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
       while (todo) {
         const int src = __ffsll((unsigned long long)todo) - 1;
         todo &= todo - 1;
-        const long long f = __shfl(first, src, kWave), count = __shfl(parts, src, kWave);
+        const long long f = lane_value((int64_t)first, src), count = lane_value((int64_t)parts, src);
         const int64_t lo = f > 0 ? f : 0;
         const int64_t last = f + count < p.items_cap ? f + count : p.items_cap;
-        const long long k = __shfl((long long)pos, src, kWave), seg = __shfl((long long)s, src, kWave);
-        const long long seg_start = __shfl((long long)start, src, kWave);
-        const long long seg_rows = __shfl((long long)length, src, kWave);
-        const bool whole = __shfl((int)fits, src, kWave) != 0;
+        const long long k = lane_value((int64_t)pos, src), seg = lane_value((int64_t)s, src);
+        const long long seg_start = lane_value((int64_t)start, src);
+        const long long seg_rows = lane_value((int64_t)length, src);
+        const bool whole = lane_value((int)fits, src) != 0;
         for (int64_t i = lo + lane; i < last; i += kWave) describe(i, f, count, k, seg, seg_start, seg_rows, whole);
       }
       continue;
@@ -609,8 +609,8 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
     while (todo) {
       const int src = __ffsll((unsigned long long)todo) - 1;
       todo &= todo - 1;
-      const long long f = __shfl(first, src, kWave), count = __shfl(parts, src, kWave);
-      const long long k = __shfl((long long)pos, src, kWave);
+      const long long f = lane_value((int64_t)first, src), count = lane_value((int64_t)parts, src);
+      const long long k = lane_value((int64_t)pos, src);
       const int64_t last = f + count < p.items_cap ? f + count : p.items_cap;
       for (int64_t i = f + lane; i < last; i += kWave) {
         if (p.item_pos) p.item_pos[i] = k;

@@ -531,8 +531,8 @@ __device__ __forceinline__ void wave_batch(const Params& p, int64_t index, int64
   while (todo) {
     const int src = __ffsll((unsigned long long)todo) - 1;
     todo &= todo - 1;
-    const int64_t ss = __shfl(s, src, kWave);
-    const int64_t a = __shfl(start, src, kWave), b = __shfl(end, src, kWave);
+    const int64_t ss = lane_value(s, src);
+    const int64_t a = lane_value(start, src), b = lane_value(end, src);
     for (int tile = 0; tile < tiles_wave; ++tile) process_segment<OP, T, VEC, FLAT, MASK, false>(p, ss, a, b, tile, nullptr);
   }
 }
