@@ -21,8 +21,10 @@
 // by a running workgroup whenever the device holds all chunks of the
 // segment at once. Segments with more chunks than that (wait_parts), and
 // chunks whose spin limit passes, skip the wait: they drop their registers
-// and k_softmax_deferred re-reads them after this kernel. No wait is
-// unbounded.
+// and k_softmax_deferred re-reads them after this kernel. A wait for chunks
+// not yet handed out also ends when the ticket counter stalls (fewer
+// workgroups resident than the plan assumed: another process on the
+// device). No wait is unbounded.
 //
 // Reference semantics: docs/semantics.md (softmax row), the reference's
 // online statistics and merge algebra (ToGPU.cpp:486-557, 435-472) restated
@@ -334,14 +336,44 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
   return all;
 }
 
-// fold_block until every slot is published or the wall-clock budget ends
-// (the decision is thread 0's, so the workgroup agrees); false on timeout.
+// A wait also ends, before its budget, once the segment still has chunks
+// not handed out (ticket counter <= last_ticket) and the ticket counter has
+// not moved over an interval of spin_ticks / kStallDivisor (100 us with the
+// default budget): every workgroup that could take them is then busy
+// (waiting, or another process holds the CUs), so waiting longer gains
+// nothing. In a free device the counter moves every few hundred
+// nanoseconds and a wait lasts 10-25 us, so the counter -- the kernel's
+// hottest atomic, which hundreds of polling waiters would slow for
+// everyone -- is read only by waits already one interval long, once per
+// interval.
+constexpr int kStallDivisor = 20;
+
+// fold_block until every slot is published, the wall-clock budget ends or
+// the ticket counter stalls before the segment's last chunk is handed out
+// (the decisions are thread 0's, so the workgroup agrees); false when the
+// wait gave up.
 __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, int d, int64_t spin_ticks,
-                                          float* lds_m, float* lds_s, uint64_t* stage) {
+                                          const int64_t* tickets, int64_t last_ticket, float* lds_m, float* lds_s,
+                                          uint64_t* stage) {
   const long long start = wall_clock64();
+  const long long interval = spin_ticks / kStallDivisor;
+  long long next_check = start + interval;
+  int64_t seen = -1;
   for (;;) {
     if (fold_block(base, count, 1, d, lds_m, lds_s, stage)) return true;
-    if (block_any(threadIdx.x == 0 && wall_clock64() - start >= spin_ticks)) return false;
+    bool give_up = false;
+    if (threadIdx.x == 0) {
+      const long long now = wall_clock64();
+      give_up = now - start >= spin_ticks;
+      if (!give_up && now >= next_check) {
+        const int64_t handed = __hip_atomic_load(const_cast<int64_t*>(tickets), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        give_up = handed == seen && handed <= last_ticket;
+        seen = handed;
+        next_check = now + interval;
+      }
+    }
+    if (block_any(give_up)) return false;
     __builtin_amdgcn_s_sleep(kPollSleep);
   }
 }
@@ -607,8 +639,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       if (!may_wait) {
         defer = true;        // more chunks than the device surely holds at once
       } else {
-        const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, lds, lds_s, stage)
-                                  : wait_fold(p.final_pairs + it.k * d, 1, p.d, p.spin_ticks, lds, lds_s, stage);
+        const int64_t last_ticket = ticket - it.c + parts - 1;
+        const int64_t* tickets = p.counters + 4;
+        const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, tickets, last_ticket,
+                                              lds, lds_s, stage)
+                                  : wait_fold(p.final_pairs + it.k * d, 1, p.d, p.spin_ticks, tickets, last_ticket,
+                                              lds, lds_s, stage);
         defer = !ready;
         // Same thread wrote lds[f] / lds_s[f] in the fold: no barrier needed.
         if (ready) {

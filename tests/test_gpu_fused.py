@@ -107,3 +107,49 @@ def test_debug_visits_and_queues(artifact_cache):
     for c in range(3):
         np.testing.assert_array_equal(np.sort(ids[c, :counts[c]]), np.flatnonzero(classes == c))
     np.testing.assert_array_equal(buffers["visits"].cpu().numpy(), np.ones(len(lengths), dtype=np.int32))
+
+
+@pytest.mark.parametrize("chunks", [24, 48])
+def test_waits_end_when_workgroups_are_short(chunks):
+    """Another process holding most CUs leaves fewer workgroups resident than
+    the plan's grid; shrinking the register-resident launch to 4 workgroups
+    through the C-ABI shows it. A segment of `chunks` chunks then has all
+    resident workgroups waiting for chunks nobody can take: the ticket
+    counter, unchanged over two checks 1/20 of the 2 ms spin bound apart,
+    ends each wait, the chunks take the re-read pass, and the result is
+    exact. Without that rule every round of 4 chunks would wait the full
+    2 ms."""
+    from gpu_helpers import check as check_result
+    from ragged import native
+    spec = native.make_spec("softmax", "bf16", "i64", 128)
+    module = native.NativeModule(0, spec)
+    capacity = int(spec.part_rows)
+    lengths = np.array([3, chunks * capacity, 100, capacity + 1, 7], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    n, b = int(offsets[-1]), len(lengths)
+    values = np.random.default_rng(chunks).normal(size=(n, 128)).astype(np.float32)
+    plan = module.plan(n, b, "classified")
+    fused = [i for i in range(plan.launches) if native.ROLES[plan.roles[i]] == "fused"]
+    assert len(fused) == 1 and plan.grid[fused[0]][0] > 4
+    plan.grid[fused[0]][0] = 4
+    x = torch.from_numpy(values).to("cuda").to(torch.bfloat16)
+    off = torch.from_numpy(offsets).to("cuda")
+    out = torch.full_like(x, float("nan"))
+    workspace = torch.zeros((int(plan.workspace_bytes),), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(2):
+        out.fill_(float("nan"))
+        start.record()
+        module.run(plan, x.data_ptr(), off.data_ptr(), out.data_ptr(), None, workspace.data_ptr(),
+                   int(plan.workspace_bytes), stream.cuda_stream)
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end))
+        check_result(out.float().cpu().numpy().astype(np.float64), x.float().cpu().numpy(), offsets, op="softmax",
+                     dtype="bf16")
+    rounds = chunks // 4
+    print(f"{chunks} chunks on 4 workgroups: {times} ms")
+    assert min(times) < 0.25 * rounds * 2.0, f"waits ran to their 2 ms bound: {times} ms for {rounds} rounds"
+    module.close()
