@@ -57,6 +57,7 @@ constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr int kTreeGroup = 32;         // register-resident softmax: chunks per first-level tree group
 constexpr int kDoneSlot = 11;          // counters slot: workgroups of the call's last kernel finished
+constexpr int kDirectDone = 64;        // up to this many active workgroups count out on kDoneSlot alone
 constexpr int32_t kStatsReady = -1;     // seg_arrive[k] once a split segment's softmax statistics are published
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 

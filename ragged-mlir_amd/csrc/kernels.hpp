@@ -414,9 +414,10 @@ __device__ __forceinline__ int64_t active_workgroups(int64_t work) {
 // End of a classified call's last kernel: every active workgroup (blockIdx <
 // `active`, all of whom read the counters first) counts itself out
 // (once its stores are complete when `drain`: what the last workgroup then
-// reads must be published); returns true in the last one. Counting is
-// two-level, because atomics on one address serialise (about 12.5 ns each
-// on MI355X): workgroup w counts at lane w % kTicketLanes (the done lanes,
+// reads must be published); returns true in the last one. Up to
+// kDirectDone workgroups count at counters[kDoneSlot] alone; more count in
+// two levels, because atomics on one address serialise (about 12.5 ns each
+// on MI355X): workgroup w at lane w % kTicketLanes (the done lanes,
 // kTicketStride apart after the ticket lanes), the last of each lane at
 // counters[kDoneSlot]. The last workgroup may still use the workspace; it
 // then calls reset_counters.
@@ -425,13 +426,20 @@ __device__ __forceinline__ bool last_out(const Params& p, int* flag_s, int64_t a
   __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned count = (unsigned)active;
-    const unsigned lanes = count < (unsigned)kTicketLanes ? count : (unsigned)kTicketLanes;
-    const unsigned lane = blockIdx.x % lanes;
-    const unsigned long long in_lane = (count - lane + lanes - 1) / lanes;   // active workgroups w = lane (mod lanes)
-    unsigned long long* lane_counter = (unsigned long long*)(p.counters + kTicketStride * (1 + kTicketLanes + lane));
     bool last = false;
-    if (atomicAdd(lane_counter, 1ull) == in_lane - 1)
-      last = atomicAdd((unsigned long long*)(p.counters + kDoneSlot), 1ull) == lanes - 1;
+    if (count <= kDirectDone) {
+      // Few workgroups: one counter serialises them in under a microsecond,
+      // and the last one learns it one round trip sooner.
+      last = atomicAdd((unsigned long long*)(p.counters + kDoneSlot), 1ull) == count - 1;
+    } else {
+      const unsigned lanes = kTicketLanes;
+      const unsigned lane = blockIdx.x % lanes;
+      const unsigned long long in_lane = (count - lane + lanes - 1) / lanes;   // active workgroups w = lane (mod lanes)
+      unsigned long long* lane_counter =
+          (unsigned long long*)(p.counters + kTicketStride * (1 + kTicketLanes + lane));
+      if (atomicAdd(lane_counter, 1ull) == in_lane - 1)
+        last = atomicAdd((unsigned long long*)(p.counters + kDoneSlot), 1ull) == lanes - 1;
+    }
     *flag_s = last ? 1 : 0;
   }
   __syncthreads();

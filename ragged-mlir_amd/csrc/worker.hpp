@@ -588,10 +588,14 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   const int lanes = active < kTicketLanes ? (int)active : kTicketLanes;
   const int lane_id = (int)(blockIdx.x % lanes);
   unsigned long long* counter = (unsigned long long*)(p.counters + kTicketStride * (1 + lane_id));
+  // Tickets are static (grid-stride, as in the short-segment schedule) when
+  // every ticket is a batch of segments in order: batches are alike, so
+  // the hand-out atomic's round trip buys no balance.
+  const bool static_tickets = direct || in_order;
   int64_t next = blockIdx.x;
   for (;;) {
     int64_t ticket = next;
-    if (!direct) {
+    if (!static_tickets) {
       __syncthreads();
       if (t == 0) ticket_s = (int64_t)atomicAdd(counter, 1ull) * lanes + lane_id;
       __syncthreads();
