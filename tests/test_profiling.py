@@ -1,0 +1,111 @@
+"""CPU tests of the rocprofv3 summariser (ragged/profiling.py; the
+reference's bench/profile.py:120-144 restated for rocprofv3) on a committed
+database whose rows were copied from real rocprofv3 runs of C1 and of the
+1 GiB copy probe on one MI355X (tests/golden/make_rocprof_fixture.py). The
+expected values are aggregated here with SQL, independently of the
+summariser's own code."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+import sqlite3
+
+import pytest
+
+from ragged import profiling
+
+DB = Path(__file__).resolve().parent / "golden" / "rocprof_c1_sample.db"
+WORKER = "k_worker<0, float, long, 4, true, false>"
+COPY_BYTES = 1 << 30
+
+
+def sql(query, *args):
+    connection = sqlite3.connect(f"file:{DB}?mode=ro", uri=True)
+    try:
+        return connection.execute(query, args).fetchall()
+    finally:
+        connection.close()
+
+
+def test_short_names():
+    assert profiling.short_name("void rg::k_worker<0, float, long, 4, true, false>(rg::Params)") == WORKER
+    assert profiling.short_name("__amd_rocclr_copyBuffer") == "__amd_rocclr_copyBuffer"
+
+
+def test_kernel_stats_from_the_trace():
+    stats = profiling.kernel_stats(DB)
+    (calls, mean, total), = sql("select count(*), avg(duration), sum(duration) from kernels where name like '%k_worker%'")
+    assert stats[WORKER]["calls"] == calls == 23
+    assert stats[WORKER]["avg_ns"] == pytest.approx(mean)
+    grand = sql("select sum(duration) from kernels")[0][0]
+    assert stats[WORKER]["pct"] == pytest.approx(100 * total / grand)
+    assert set(stats) == {WORKER, "k_classify<long>"}
+
+
+def test_counters_copy_factor_and_traffic():
+    fetch = profiling.counter_per_dispatch(DB, "FETCH_SIZE")
+    (dispatches, mean), = sql("select count(*), avg(value) from counters_collection "
+                              "where counter_name = 'FETCH_SIZE' and kernel_name like '%k_worker%'")
+    assert fetch[WORKER]["dispatches"] == dispatches == 8 and fetch[WORKER]["mean"] == pytest.approx(mean)
+    factor = profiling.copy_factor(DB, DB, COPY_BYTES, "copyBuffer")
+    (copy_fetch,), = sql("select avg(value) from counters_collection where counter_name = 'FETCH_SIZE' "
+                         "and kernel_name like '%copyBuffer%'")
+    (copy_write,), = sql("select avg(value) from counters_collection where counter_name = 'WRITE_SIZE' "
+                         "and kernel_name like '%copyBuffer%'")
+    # The copy reads and writes 1 GiB: WRITE_SIZE counts KiB exactly, FETCH_SIZE half of the bytes.
+    assert copy_write == 1 << 20 and factor["write_bytes_per_unit"] == 1024.0
+    assert factor["fetch_bytes_per_unit"] == pytest.approx(COPY_BYTES / copy_fetch) == pytest.approx(2048, rel=1e-4)
+    traffic = profiling.traffic(DB, DB, "k_worker", factor)
+    (worker_write,), = sql("select avg(value) from counters_collection where counter_name = 'WRITE_SIZE' "
+                           "and kernel_name like '%k_worker%'")
+    assert traffic["read_bytes"] == pytest.approx(mean * COPY_BYTES / copy_fetch)
+    assert traffic["write_bytes"] == pytest.approx(worker_write * 1024)
+    assert traffic["bytes"] == pytest.approx(traffic["read_bytes"] + traffic["write_bytes"])
+
+
+def test_resources_and_report(tmp_path, capsys):
+    resources = profiling.kernel_resources(DB)
+    vgpr, lds, grid, group = sql("select vgpr_count, lds_size, grid_x, workgroup_x from kernels "
+                                 "where name like '%k_worker%' limit 1")[0]
+    assert resources[WORKER]["vgpr_count"] == vgpr and resources[WORKER]["lds_size"] == lds
+    factor = profiling.copy_factor(DB, DB, COPY_BYTES, "copyBuffer")
+    roles = {"classify": {"bytes": 80_008}, "worker": {"bytes": 2_600_000}}
+    lines = profiling.report(DB, DB, DB, DB, factor, roles, "c1")
+    row = next(line for line in lines if line.startswith("| worker |"))
+    cells = [c.strip() for c in row.strip("|").split("|")]
+    mean_us = profiling.kernel_stats(DB)[WORKER]["avg_ns"] / 1e3
+    assert float(cells[3]) == pytest.approx(mean_us, abs=0.005)
+    assert cells[5].startswith(f"{2_600_000 / (mean_us * 1e-6) / 1e9:.0f} (")
+    traffic = profiling.traffic(DB, DB, "k_worker", factor)
+    assert float(cells[8]) == pytest.approx(traffic["bytes"] / 2_600_000, abs=0.0005)
+    (occupancy,), = sql("select avg(value) from counters_collection where counter_name = 'OccupancyPercent' "
+                        "and kernel_name like '%k_worker%'")
+    assert float(cells[9]) == pytest.approx(occupancy, abs=0.05)
+    assert int(cells[13]) == 2 * vgpr and int(cells[18]) == grid // group
+    # The command line: the same table from a bench.py --details file.
+    details = tmp_path / "details.json"
+    details.write_text(json.dumps({"records": [{"select": "auto", "op": "sum", "kernels": roles}]}))
+    assert profiling.main(["report", "--stats", str(DB), "--fetch", str(DB), "--write", str(DB), "--occupancy",
+                           str(DB), "--copy-fetch", str(DB), "--copy-write", str(DB), "--copy-bytes",
+                           str(COPY_BYTES), "--copy-kernel", "copyBuffer", "--details", str(details),
+                           "--title", "c1"]) == 0
+    assert row in capsys.readouterr().out
+
+
+def test_csv_formats(tmp_path):
+    """rocprofv3 --output-format csv: kernel stats and counter collection."""
+    stats = tmp_path / "c1_kernel_stats.csv"
+    stats.write_text('"Name","Calls","TotalDurationNs","AverageNs","Percentage"\n'
+                     f'"void rg::{WORKER}(rg::Params)",4,40000,10000,80.0\n'
+                     '"void rg::k_classify<long>(rg::Params)",4,10000,2500,20.0\n')
+    table = profiling.kernel_stats(stats)
+    assert table[WORKER] == pytest.approx({"calls": 4, "total_ns": 40000.0, "avg_ns": 10000.0, "pct": 80.0})
+    counters = tmp_path / "c1_counter_collection.csv"
+    counters.write_text('"Dispatch_Id","Kernel_Name","Counter_Name","Counter_Value"\n'
+                        f'1,"void rg::{WORKER}(rg::Params)","FETCH_SIZE",10\n'
+                        f'1,"void rg::{WORKER}(rg::Params)","FETCH_SIZE",5\n'
+                        f'2,"void rg::{WORKER}(rg::Params)","FETCH_SIZE",7\n'
+                        f'2,"void rg::{WORKER}(rg::Params)","WRITE_SIZE",99\n')
+    # Rows of one dispatch (one per channel on some ROCm versions) add up.
+    assert profiling.counter_per_dispatch(counters, "FETCH_SIZE")[WORKER] == {"dispatches": 2, "sum": 22.0,
+                                                                              "mean": 11.0}
