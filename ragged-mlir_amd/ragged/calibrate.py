@@ -30,7 +30,7 @@ Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
   L2 capacity (``measure`` records it) and the refitted one.
 
     python -m ragged.calibrate measure --suite train --out train.jsonl
-    python -m ragged.calibrate fit train.jsonl --out cost_model.json [--heldout heldout2.jsonl]
+    python -m ragged.calibrate fit train.jsonl [more.jsonl ...] --out cost_model.json [--heldout heldout5.jsonl]
     python -m ragged.calibrate evaluate heldout.jsonl [--model cost_model.json]
     python -m ragged.calibrate transfer train.jsonl heldout.jsonl --out refit.json [--model cost_model.json]
 """
@@ -86,21 +86,21 @@ def _grid(ds, elements, segments, seed0, count, seed_grid):
     return cases
 
 
-SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4")
+SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5")
 
 
 def suite(name: str) -> list[Case]:
     """The fixed shape suites. The held-out suites share no feature width,
     size or segment count with either train suite or with each other;
-    heldout, heldout2 and heldout3 reach beyond the 256 MiB Infinity Cache
-    (working sets up to 512, 384 and 320 MiB). Each was frozen before the fit
-    it scores and scored once for it: ``heldout3`` for the shipped model
-    (fitted on ``train``); ``heldout4`` for a fit on ``train_dense`` (five
-    segment counts instead of three), which scored lower on every held-out
-    suite and was not shipped; ``heldout2`` for a fit of the eight-term
-    model, whose misses shaped the current terms; ``heldout`` after several
-    earlier refits. Both train suites hold feature widths whose lane access
-    is 4 or 8 bytes (5, 10) besides 16-byte ones."""
+    heldout, heldout2, heldout3 and heldout5 reach beyond the 256 MiB
+    Infinity Cache (working sets up to 512, 384, 320 and 384 MiB). Each was
+    frozen before the fit it scores and scored once for it: ``heldout5`` for
+    the shipped model (``train`` and ``train_dense`` pooled); ``heldout3``
+    for a fit on ``train`` alone; ``heldout4`` for a fit on ``train_dense``
+    alone; ``heldout2`` for a fit of the eight-term model, whose misses
+    shaped the current terms; ``heldout`` after several earlier refits.
+    Both train suites hold feature widths whose lane access is 4 or 8 bytes
+    (5, 10) besides 16-byte ones."""
     if name == "train":
         return _grid(ds=(1, 2, 5, 8, 10, 32, 128), elements=(1 << 18, 1 << 21, 1 << 24),
                      segments=(256, 4096, 65536), seed0=1000, count=330, seed_grid=11)
@@ -119,6 +119,9 @@ def suite(name: str) -> list[Case]:
     if name == "heldout4":
         return _grid(ds=(9, 14, 20, 56, 112), elements=(7 << 18, 7 << 21, 7 << 22),
                      segments=(640, 3072, 20480), seed0=17000, count=150, seed_grid=59)
+    if name == "heldout5":
+        return _grid(ds=(11, 18, 28, 80, 144), elements=(6 << 18, 6 << 21, 6 << 23),
+                     segments=(384, 2560, 40960), seed0=21000, count=150, seed_grid=61)
     raise ValueError(f"suite must be one of {SUITES}")
 
 
@@ -418,7 +421,7 @@ def main(argv=None) -> int:
     m.add_argument("--out", type=Path, required=True)
     m.add_argument("--limit", type=int, help="measure at most this many cases of the suite")
     f = sub.add_parser("fit")
-    f.add_argument("results", type=Path)
+    f.add_argument("results", type=Path, nargs="+", help="train measurements (several files are pooled)")
     f.add_argument("--out", type=Path, required=True)
     f.add_argument("--heldout", type=Path, help="held-out measurements to evaluate the fit on (recorded only)")
     f.add_argument("--check", type=Path, action="append", default=[],
@@ -440,9 +443,9 @@ def main(argv=None) -> int:
         print(f"[calibrate] measured {count} cases in {time.perf_counter() - started:.1f}s", flush=True)
         return 0
     if args.command == "fit":
-        records = load(args.results)
+        records = [record for path in args.results for record in load(path)]
         data = fit(records)
-        data["calibration"]["train_file"] = args.results.name
+        data["calibration"]["train_file"] = " + ".join(path.name for path in args.results)
         data["calibration"]["device"] = ("gfx950 (the library's only target); L2 MiB measured: "
                                          f"{sorted({r['l2_mib'] for r in records if r.get('l2_mib')})}")
         data["calibration"]["command"] = "python -m ragged.calibrate " + " ".join(
