@@ -70,7 +70,7 @@ def device_l2_mib(values) -> float | None:
 def _span(tensor) -> tuple[int, int]:
     """[first byte, one past the last byte) of a contiguous tensor."""
     start = tensor.data_ptr()
-    return start, start + tensor.numel() * tensor.element_size()
+    return start, start + tensor.nbytes
 
 
 def _spans_overlap(left: tuple[int, int], right: tuple[int, int]) -> bool:
@@ -184,7 +184,8 @@ class CompiledProgram:
                 raise ValidationError(f"{name} must be row-major contiguous")
             if tensor.requires_grad:
                 raise ValidationError("autograd is outside the supported forward-only contract")
-        if values.device != offsets.device or values.device != out.device:
+        device = values.get_device()
+        if offsets.get_device() != device or out.get_device() != device:
             raise ValidationError("values, offsets and out must use the same device")
         if values.ndim != 2 or values.shape[1] != self.spec.feature_dim:
             raise ValidationError("values must have shape [N, static D]")
@@ -221,7 +222,7 @@ class CompiledProgram:
             if mask.dtype != torch.float32 or tuple(mask.shape) != tuple(values.shape):
                 raise ValidationError("mask must have f32 dtype and exactly values shape [N,D]; "
                                       "broadcasting is unsupported")
-            if mask.device != values.device:
+            if mask.get_device() != device:
                 raise ValidationError("mask must use the values device")
             mask_span = _span(mask)
             if _spans_overlap(mask_span, out_span) or _spans_overlap(mask_span, offsets_span):
@@ -239,6 +240,9 @@ class CompiledProgram:
 
     def _module(self, device: int) -> native.NativeModule:
         key = (device, self._digest)
+        module = _modules.get(key)
+        if module is not None:
+            return module
         with _lock:
             module = _modules.get(key)
             if module is None:
@@ -361,9 +365,10 @@ class CompiledProgram:
         started = time.perf_counter()
         if b == 0 and not checked:
             return self._report(started, mode=mode, selected=selected, selection=selection)
-        device = values.device.index if values.device.index is not None else torch.cuda.current_device()
-        # Switch devices only when the tensors are not on the current one.
-        switch = device != torch.cuda.current_device()
+        # The tensors' device (validated: all on one ROCm device), and a
+        # switch only when it is not the current one.
+        device = values.get_device()
+        switch = device != torch._C._cuda_getDevice()
         with torch.cuda.device(device) if switch else contextlib.nullcontext():
             runs = _device_runs.get((device, self.spec.chip))
             if runs is None:
