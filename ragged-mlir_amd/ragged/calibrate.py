@@ -3,9 +3,10 @@
 Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
 272-305) and ``bench/suite.py`` (:42-60) for this build:
 
-* Two synthetic shape suites are fixed in code before any fit: ``train``
-  and ``heldout``, drawn from disjoint feature widths, sizes and seeds, so
-  no held-out shape is seen while fitting.
+* Synthetic shape suites are fixed in code before any fit (``suite``):
+  train suites and held-out suites drawn from disjoint feature widths,
+  sizes, segment counts and seeds, so no held-out shape is seen while
+  fitting.
 * ``measure`` times both schedules (classified, block per segment) of every
   case on the current GPU: complete ``program.run`` calls bracketed by
   events on the calling stream, warm (median of repeated batches) and cold
@@ -18,11 +19,16 @@ Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
   resumes.
 * ``fit`` solves, per operation family and schedule, a nonnegative least
   squares problem on relative error (each row divided by its measured
-  time) over all terms, reports its leave-one-shape-out error, and then
-  picks the decision margin that maximises the share of training cases
-  within 3% of the faster schedule.
-* ``evaluate`` reports, for a suite's measurements, how many choices fall
-  within 3% of the faster measured schedule, warm and (where measured) cold.
+  time) over all terms, on the cases where ``run(select="auto")`` consults
+  the model (not those whose max_len sends them to the short-segment
+  schedule), reports its leave-one-shape-out error, and then picks per
+  family the decision margin that maximises the share of the family's
+  training cases within 3% of the faster schedule.
+* ``evaluate`` reports, for a suite's measurements, how many of the
+  schedules ``run(select="auto")`` takes fall within 3% of the faster
+  measured schedule, warm and (where measured) cold: the short-segment
+  rule first, then the model. (``measure`` times the forced classified
+  schedule, which is the short-segment one exactly when that rule holds.)
 * ``transfer`` (the reference's ``calibrate.py transfer``, :229-272) takes
   the train and held-out measurements of another device (or ROCm, or
   firmware), refits there (written to ``--out``) and reports on its
@@ -86,21 +92,23 @@ def _grid(ds, elements, segments, seed0, count, seed_grid):
     return cases
 
 
-SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5")
+SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5", "heldout6")
 
 
 def suite(name: str) -> list[Case]:
     """The fixed shape suites. The held-out suites share no feature width,
     size or segment count with either train suite or with each other;
-    heldout, heldout2, heldout3 and heldout5 reach beyond the 256 MiB
-    Infinity Cache (working sets up to 512, 384, 320 and 384 MiB). Each was
-    frozen before the fit it scores and scored once for it: ``heldout5`` for
-    the shipped model (``train`` and ``train_dense`` pooled); ``heldout3``
-    for a fit on ``train`` alone; ``heldout4`` for a fit on ``train_dense``
-    alone; ``heldout2`` for a fit of the eight-term model, whose misses
-    shaped the current terms; ``heldout`` after several earlier refits.
-    Both train suites hold feature widths whose lane access is 4 or 8 bytes
-    (5, 10) besides 16-byte ones."""
+    heldout, heldout2, heldout3, heldout5 and heldout6 reach beyond the 256
+    MiB Infinity Cache (working sets up to 512, 384, 320, 384 and 576 MiB).
+    Each was frozen before the fit it scores and scored once for it:
+    ``heldout6`` for the shipped model (fitted on every other suite pooled:
+    their measurements on the shipped library); ``heldout5`` for a fit on
+    the two train suites; ``heldout3`` for a fit on ``train`` alone;
+    ``heldout4`` for a fit on ``train_dense`` alone; ``heldout2`` for a fit
+    of the eight-term model, whose misses shaped the nine-term one;
+    ``heldout`` after several earlier refits. The train suites hold feature
+    widths whose lane access is 4 or 8 bytes (5, 10) besides 16-byte ones;
+    the earlier held-out suites, now training data, add many more."""
     if name == "train":
         return _grid(ds=(1, 2, 5, 8, 10, 32, 128), elements=(1 << 18, 1 << 21, 1 << 24),
                      segments=(256, 4096, 65536), seed0=1000, count=330, seed_grid=11)
@@ -122,6 +130,9 @@ def suite(name: str) -> list[Case]:
     if name == "heldout5":
         return _grid(ds=(11, 18, 28, 80, 144), elements=(6 << 18, 6 << 21, 6 << 23),
                      segments=(384, 2560, 40960), seed0=21000, count=150, seed_grid=61)
+    if name == "heldout6":
+        return _grid(ds=(13, 22, 36, 72, 176), elements=(9 << 18, 9 << 21, 9 << 23),
+                     segments=(448, 5120, 57344), seed0=25000, count=150, seed_grid=67)
     raise ValueError(f"suite must be one of {SUITES}")
 
 
@@ -325,12 +336,34 @@ def fit_family(records: list[dict], schedule: str) -> tuple[np.ndarray, float]:
     return _fit_relative(rows, times, every), error
 
 
+_alone: dict[tuple, int] = {}
+
+
+def short_segments(record: dict) -> bool:
+    """Whether ``run(select="auto")`` sends the record's call to the
+    short-segment schedule without consulting the model (its max_len lets
+    one lane or lane group reduce every segment alone): the runtime's rule,
+    from the library's defaults for the record's specialisation (the
+    measured programs use default thresholds and i64 offsets)."""
+    key = (record["op"], record["dtype"], record["d"])
+    if key not in _alone:
+        from . import native
+        spec = native.make_spec(record["op"], record["dtype"], "i64", record["d"])
+        _alone[key] = int(spec.alone_rows) if spec.t_wave > 0 else 0
+    return 0 < _alone[key] and record["max_len"] <= _alone[key]
+
+
 def choices(model: CostModel, records: list[dict], device_l2: bool = False) -> list[tuple[dict, str]]:
-    """The model's schedule for every record; with ``device_l2``, given the
-    L2 capacity the record was measured with (when it holds one) instead of
-    the model's own."""
+    """The schedule ``run(select="auto")`` takes for every record: the
+    short-segment schedule (measured as "classified") where its rule holds,
+    else the model's choice; with ``device_l2``, the model is given the L2
+    capacity the record was measured with (when it holds one) instead of
+    its own."""
     out = []
     for record in records:
+        if short_segments(record):
+            out.append((record, "classified"))
+            continue
         element = 2 if record["dtype"] == "bf16" else 4
         l2_mib = record.get("l2_mib") if device_l2 else None
         chosen, _ = model.choose(record["op"], record["n"], record["b"], record["d"], record["max_len"], element,
@@ -364,8 +397,9 @@ def evaluate(model: CostModel, records: list[dict], device_l2: bool = False, col
 def fit(records: list[dict]) -> dict:
     """The cost model file for ``records`` (train measurements)."""
     coefficients, errors = {}, {}
+    modelled = [r for r in records if not short_segments(r)]
     for name in FAMILIES:
-        subset = [r for r in records if _family(r) == name]
+        subset = [r for r in modelled if _family(r) == name]
         if len(subset) < TERMS:
             raise ValueError(f"too few {name} measurements to fit ({len(subset)})")
         coefficients[name], errors[name] = {}, {}
@@ -373,24 +407,31 @@ def fit(records: list[dict]) -> dict:
             coef, error = fit_family(subset, schedule)
             coefficients[name][schedule] = [round(float(c), 6) for c in coef]
             errors[name][schedule] = round(error, 4)
-    data = {"version": VERSION, "coefficients": coefficients, "margin": 0.0, "l2_mib": 32.0, "mall_mib": 256.0,
-            "calibration": {}}
-    # Margin: classify only when predicted faster by this fraction; pick the
-    # one that maximises within-3% choices on the training set.
-    best_margin, best_share = 0.0, -1.0
-    for margin in np.arange(0.0, 0.5, 0.01):
-        data["margin"] = float(round(margin, 2))
-        share = evaluate(CostModel.from_dict(data), records)["share"]
-        if share > best_share + 1e-12:
-            best_margin, best_share = data["margin"], share
-    data["margin"] = best_margin
+    data = {"version": VERSION, "coefficients": coefficients, "margins": {name: 0.0 for name in FAMILIES},
+            "l2_mib": 32.0, "mall_mib": 256.0, "calibration": {}}
+    # Margins: a family classifies only when predicted faster by its margin;
+    # each is the one that maximises within-3% choices on the family's
+    # training cases (the smallest such).
+    for name in FAMILIES:
+        subset = [r for r in records if _family(r) == name]
+        best_margin, best_share = 0.0, -1.0
+        for margin in np.arange(0.0, 0.5, 0.01):
+            data["margins"][name] = float(round(margin, 2))
+            share = evaluate(CostModel.from_dict(data), subset)["share"]
+            if share > best_share + 1e-12:
+                best_margin, best_share = data["margins"][name], share
+        data["margins"][name] = best_margin
+    best_share = evaluate(CostModel.from_dict(data), records)["share"]
     libraries = sorted({r["library_sha256"] for r in records if r.get("library_sha256")})
     data["calibration"] = {
         "status": "fitted on MI355X measurements (python -m ragged.calibrate fit)",
         "library_sha256": libraries[0] if len(libraries) == 1 else libraries,
-        "terms": "t_us = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall + c8*W*A",
-        "method": "per family and schedule: NNLS on relative error over all terms (leave-one-shape-out error "
-                  "reported); margin maximising training choices within 3% of the faster schedule",
+        "terms": "t_us = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall + c8*W*A "
+                 "+ c9*W*U + c10*S*U",
+        "method": "per family and schedule: NNLS on relative error over all terms, on the cases the runtime "
+                  "models (leave-one-shape-out error reported); per family the margin maximising the family's "
+                  "training choices within 3% of the faster schedule; choices scored as run(select='auto') "
+                  "makes them (short-segment rule first)",
         "train_cases": len(records), "leave_one_shape_out_error": errors, "train_within_3pct": best_share}
     if all("us_cold" in r for r in records):
         data["calibration"]["train_within_3pct_cold"] = evaluate(CostModel.from_dict(data), records, cold=True)["share"]

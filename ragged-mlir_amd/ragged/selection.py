@@ -4,14 +4,15 @@ Same decision rule as the reference's ``python/ragged/selection.py``
 (:56-126): predict the complete-call time of each schedule from host-known
 statistics (N, B, D, element size and the caller's longest segment L) with a
 linear model per operation family and schedule, and classify only when that
-is predicted faster by ``margin``; without L keep classification. The
+is predicted faster by the family's margin; without L keep classification. The
 families are the reference's {reduce, softmax} plus ``softmax_fused``: a
 softmax whose classified schedule is the register-resident worker pays a
 per-segment cost the streaming worker does not, so it gets its own fit.
 
-The terms are re-derived for MI355X (model version 5, nine terms, µs):
+The terms are re-derived for MI355X (model version 6, eleven terms, µs):
 
     t = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall + c8*W*A
+          + c9*W*U + c10*S*U
 
 W = MiB the call moves (rows read; rows written for softmax, B result rows
 for sum/max); S = L*D*element_bytes / 2^20, the MiB the one workgroup that
@@ -26,6 +27,17 @@ has two cache levels of very different size in front of HBM. A = 16 /
 access bytes - 1, where a lane's access is the mapping's vector (16 bytes
 for D dividing or divided by the 16-byte vector, else the largest power of
 two of elements dividing D): the extra cost per MiB of narrower accesses.
+U = 1/u - 1 for the row mapping's lane utilisation u (a row's vectors over
+the lanes that hold it: D = 80 f32 is 20 vectors on 32 lanes, u = 0.625),
+0 for the flat mapping: idle lanes cost the streaming rate of every
+workgroup (W) and of the one that owns the longest segment (S).
+
+Each family has its own margin (a register-resident softmax pays three
+more launches than its streaming counterpart, so the schedules' fixed
+costs differ by family). The runtime consults the model only when the
+caller's max_len does not let one lane or lane group reduce every segment
+alone: those calls take the one-launch short-segment schedule
+(``CompiledProgram.run``), which the model is not fitted on.
 """
 from __future__ import annotations
 
@@ -40,8 +52,8 @@ from .errors import CacheMismatch
 MODEL_PATH = Path(__file__).with_name("cost_model.json")
 SCHEDULES = ("classified", "naive")
 FAMILIES = ("reduce", "softmax", "softmax_fused")
-TERMS = 9
-VERSION = 5
+TERMS = 11
+VERSION = 6
 
 
 def family(op: str, fused: bool = False) -> str:
@@ -52,14 +64,17 @@ def family(op: str, fused: bool = False) -> str:
 
 def features(n: int, b: int, d: int, max_len: int, element_bytes: int = 4, op: str = "sum",
              l2_mib: float = 32.0, mall_mib: float = 256.0, flat: bool = False) -> tuple[float, ...]:
-    """The nine prediction terms for one call."""
+    """The eleven prediction terms for one call."""
     row = d * element_bytes
     rows = n * row / 2**20
     output_rows = n if op == "softmax" else b
     moved = rows + output_rows * row / 2**20
+    longest = max_len * row / 2**20
     segments = b / 1000.0
-    return (1.0, moved, max_len * row / 2**20, segments, segments if flat else 0.0, segments * row / 1024,
-            max(0.0, moved - l2_mib), max(0.0, moved - mall_mib), moved * (16 / access_bytes(d, element_bytes) - 1))
+    idle = 0.0 if flat else 1.0 / lane_utilisation(d, element_bytes) - 1.0
+    return (1.0, moved, longest, segments, segments if flat else 0.0, segments * row / 1024,
+            max(0.0, moved - l2_mib), max(0.0, moved - mall_mib), moved * (16 / access_bytes(d, element_bytes) - 1),
+            moved * idle, longest * idle)
 
 
 def access_bytes(d: int, element_bytes: int) -> int:
@@ -73,10 +88,22 @@ def access_bytes(d: int, element_bytes: int) -> int:
     return vec * element_bytes
 
 
+def lane_utilisation(d: int, element_bytes: int) -> float:
+    """Share of the lanes holding a row that hold data in the row mapping of
+    the default geometry (Optimizations.geometry): ceil(D / vec) vectors on
+    the next power of two of lanes (at most 64, several passes beyond)."""
+    vec = access_bytes(d, element_bytes) // element_bytes
+    vectors = -(-d // vec)
+    lanes = 1
+    while lanes < vectors and lanes < 64:
+        lanes *= 2
+    return vectors / (lanes * -(-vectors // lanes))
+
+
 @dataclass(frozen=True)
 class CostModel:
     coefficients: dict[str, dict[str, tuple[float, ...]]]
-    margin: float
+    margins: dict[str, float]
     calibration: dict[str, Any]
     l2_mib: float = 32.0
     mall_mib: float = 256.0
@@ -88,16 +115,16 @@ class CostModel:
                 raise CacheMismatch("unsupported cost model version")
             coefficients = {name: {schedule: tuple(float(v) for v in data["coefficients"][name][schedule])
                                    for schedule in SCHEDULES} for name in FAMILIES}
-            margin = float(data["margin"])
+            margins = {name: float(data["margins"][name]) for name in FAMILIES}
             l2_mib, mall_mib = float(data["l2_mib"]), float(data["mall_mib"])
         except (KeyError, TypeError, ValueError) as exc:
             raise CacheMismatch(f"invalid cost model: {exc}") from exc
         if (any(len(values) != TERMS or any(v < 0 or not math.isfinite(v) for v in values)
                 for schedules in coefficients.values() for values in schedules.values())
-                or not 0 <= margin < 1 or not l2_mib > 0 or not mall_mib > 0):
-            raise CacheMismatch(f"cost model coefficients must be {TERMS} nonnegative terms, margin in [0, 1) "
+                or not all(0 <= m < 1 for m in margins.values()) or not l2_mib > 0 or not mall_mib > 0):
+            raise CacheMismatch(f"cost model coefficients must be {TERMS} nonnegative terms, margins in [0, 1) "
                                 "and positive cache capacities")
-        return cls(coefficients, margin, dict(data.get("calibration", {})), l2_mib, mall_mib)
+        return cls(coefficients, margins, dict(data.get("calibration", {})), l2_mib, mall_mib)
 
     @classmethod
     def load(cls, path: Path = MODEL_PATH) -> "CostModel":
@@ -119,7 +146,7 @@ class CostModel:
             raise ValueError("l2_mib must be a positive capacity in MiB")
         classified = self.predict("classified", op, n, b, d, max_len, element_bytes, l2_mib, fused, flat)
         naive = self.predict("naive", op, n, b, d, max_len, element_bytes, l2_mib, fused, flat)
-        selected = "classified" if classified < naive * (1 - self.margin) else "naive"
+        selected = "classified" if classified < naive * (1 - self.margins[family(op, fused)]) else "naive"
         return selected, {"max_len": max_len, "l2_mib": self.l2_mib if l2_mib is None else l2_mib,
                           "predicted_us": {"classified": round(classified, 2), "naive": round(naive, 2)}}
 

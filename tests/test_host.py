@@ -18,7 +18,7 @@ from ragged import ProgramSpec
 from ragged import native
 from ragged.errors import RuntimeUnavailable, ValidationError
 from ragged.optimizations import Optimizations
-from ragged.selection import access_bytes, features
+from ragged.selection import access_bytes, features, lane_utilisation
 from ragged.validation import CONDITIONS, I64_MAX, raise_for_status
 from ragged.workloads import describe, make_lengths, offsets_from_lengths, reference_values, sha256
 
@@ -157,9 +157,10 @@ def test_status_decoding_known_answers():
 def test_cost_model_features_known_answer():
     # N = 2^20 rows, B = 1024, D = 4 f32 (16-byte rows), L = 2^14: W = 16 MiB of rows read + 1024
     # result rows = 16.015625 MiB; S = 2^14*16/2^20 = 0.25 MiB; B/1000 = 1.024; row mapping (F = 0);
-    # R*B/1000 = 1.024 * 16/1024; the working set is under the 32 MiB L2; 16-byte accesses (A = 0).
+    # R*B/1000 = 1.024 * 16/1024; the working set is under the 32 MiB L2; 16-byte accesses (A = 0);
+    # one 16-byte vector per row on one lane (u = 1, U = 0).
     assert features(2**20, 1024, 4, 2**14, 4, "sum") == (1.0, 16.015625, 0.25, 1.024, 0.0, 1.024 * 16 / 1024,
-                                                          0.0, 0.0, 0.0)
+                                                          0.0, 0.0, 0.0, 0.0, 0.0)
     assert features(2**20, 1024, 4, 2**14, 4, "sum", flat=True)[4] == 1.024
     # Softmax writes N rows: 128 MiB of rows at D=32 f32 -> 256 MiB moved.
     f = features(2**20, 1024, 32, 2**14, 4, "softmax")
@@ -168,6 +169,14 @@ def test_cost_model_features_known_answer():
     # (A = 3), D=2 f32 and D=4 bf16 the flat 16-byte vector (A = 0).
     assert [access_bytes(d, e) for d, e in ((3, 4), (6, 4), (10, 2), (2, 4), (4, 2), (12, 2))] == [4, 8, 4, 16, 16, 8]
     assert features(1000, 10, 3, 100, 4, "sum")[8] == pytest.approx(3 * features(1000, 10, 3, 100, 4, "sum")[1])
+    # Lane utilisation of the row mapping: D=80 f32 is 20 vectors on 32 lanes (u = 0.625, U = 0.6),
+    # D=13 f32 13 on 16, D=176 bf16 22 on 32, D=1024 f32 256 vectors in 4 passes of 64 lanes (u = 1);
+    # W*U and S*U carry U, zero for the flat mapping.
+    assert [lane_utilisation(d, e) for d, e in ((80, 4), (13, 4), (176, 2), (1024, 4), (128, 2))] == [
+        0.625, 13 / 16, 22 / 32, 1.0, 1.0]
+    f = features(1 << 20, 4096, 80, 1000, 4, "sum")
+    assert f[9] == pytest.approx(0.6 * f[1]) and f[10] == pytest.approx(0.6 * f[2])
+    assert features(1 << 20, 4096, 2, 1000, 4, "sum", flat=True)[9:] == (0.0, 0.0)
     # The same width as the geometry the programs are built with.
     for dtype, element in (("f32", 4), ("bf16", 2)):
         for d in range(1, 300):
