@@ -20,7 +20,12 @@ Every measured configuration first passes the oracle (max bit-exact,
 sum/softmax within tolerance) on a sample of its segments.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c5] [--op OP] [--seeds S,..]
-                    [--cold [write|read]] [--all] [--details FILE] [--no-cpu]
+                    [--cold [write|read]] [--all] [--details FILE] [--timeline FILE] [--no-cpu]
+
+``--timeline`` records one further call of every register-resident softmax
+measured with its item trace on and writes the summary: per item class the
+phase durations, workgroups live and merging over the call, and where each
+chunk class's merge time goes (ragged.profiling.item_timeline).
 """
 from __future__ import annotations
 
@@ -357,10 +362,31 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
                 "n": workload.n, "b": workload.b, "d": workload.d, "dtype": workload.dtype,
                 "offsets_dtype": workload.offsets_dtype, "max_len": workload.max_len,
                 "kernel_names": list(report.kernel_names), "grids": [list(g) for g in report.grids]})
+            if args.timeline and plan.fused:
+                results[-1]["timeline"] = item_trace(torch, program, module, plan, x, off, out, select, max_len)
+                split = {name: entry.get("merge_split") for name, entry in results[-1]["timeline"]["classes"].items()}
+                log(f"[bench] {workload.name} {op} {select}: item timeline merge split {json.dumps(split)}")
             log(f"[bench] {workload.name} {op} {select}: host run() median/max us {host_us[0] if host_us else None}")
             log(f"[bench] {workload.name} {op} {select}: {ms * 1e3:.1f} us/call, {gbps:.0f} GB/s "
                 f"({100 * gbps / PEAK_GBPS:.1f}% of peak); kernels {json.dumps(kernels)}")
     return results, workload
+
+
+def item_trace(torch, program, module, plan, x, off, out, select, max_len) -> dict:
+    """One call with the register-resident softmax's item trace on
+    (rg_module_set_trace), summarised by ragged.profiling.item_timeline."""
+    from ragged import native, profiling
+    records = int(plan.items_cap + plan.b)
+    trace = torch.zeros((records, 8), dtype=torch.int64, device=x.device)
+    torch.cuda.synchronize()
+    module.set_trace(trace.data_ptr(), records)
+    try:
+        program.run(x, off, out, select=select, max_len=max_len)
+        torch.cuda.synchronize()
+    finally:
+        module.set_trace(None)
+    return profiling.item_timeline(trace.cpu().numpy(), native.device_clock_khz(x.device.index or 0),
+                                   int(plan.part_rows))
 
 
 def copy_probe(torch, mib: int, steps: int) -> int:
@@ -412,6 +438,9 @@ def main(argv=None) -> int:
                         help="measure only this op of the workload (c2 holds sum and max)")
     parser.add_argument("--all", action="store_true", help="also measure forced classified and naive schedules")
     parser.add_argument("--details", type=Path, help="write every measured record as JSON to this file")
+    parser.add_argument("--timeline", type=Path,
+                        help="record one call's item trace of the register-resident softmax and write its summary "
+                             "(ragged.profiling.item_timeline) as JSON to this file")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--copy-probe", type=int, metavar="MIB",
                         help="instead: time a plain device copy of MIB MiB (--steps times), the known-size "
@@ -476,6 +505,10 @@ def main(argv=None) -> int:
         args.details.parent.mkdir(parents=True, exist_ok=True)
         args.details.write_text(json.dumps({"line": line, "records": records, "cpu_baselines": variants},
                                            indent=1) + "\n")
+    if args.timeline:
+        args.timeline.parent.mkdir(parents=True, exist_ok=True)
+        args.timeline.write_text(json.dumps([{key: r[key] for key in ("workload", "op", "select", "seed", "timeline")}
+                                             for r in records if "timeline" in r], indent=1) + "\n")
     print(json.dumps(line), flush=True)
     return 0
 

@@ -183,6 +183,13 @@ def uses_fused(spec: Spec) -> bool:
     return status == 1
 
 
+def device_clock_khz(device: int = 0) -> int:
+    """Rate of the device wall clock (the timeline records' ticks), in kHz."""
+    khz = ctypes.c_int64(0)
+    _check(library().rg_device_clock_khz(device, ctypes.byref(khz)), "rg_device_clock_khz")
+    return int(khz.value)
+
+
 class NativeModule:
     """One kernel specialisation on one device (the reference's DriverModule)."""
 

@@ -17,6 +17,11 @@ summarises Nsight Compute metrics) for rocprofv3 output on gfx950:
   FETCH_SIZE / WRITE_SIZE runs and an occupancy run (OccupancyPercent,
   MeanOccupancyPerCU, VALUBusy, MemUnitStalled) plus the algorithmic bytes a
   ``bench.py --details`` file records per kernel role.
+* ``item_timeline``: the register-resident softmax's item trace (one call
+  under ``rg_module_set_trace``, ``bench.py --timeline``) reduced to each
+  item class's phase durations and workgroup time, how many workgroups were
+  live and merging over the call, and, per chunk class, where a chunk's merge
+  time goes.
 
 Both output formats are read: the SQLite database rocprofv3 writes by
 default (``*_results.db``, views ``kernels`` and ``counters_collection``) and
@@ -214,6 +219,89 @@ def report(stats_db: Path, fetch_db: Path, write_db: Path, occupancy_db: Path, f
                   "descriptor's register granule as 4; gfx950 wave64 allocates 8 per granule, which the compiler's "
                   "resource remarks confirm). Occupancy counters come from a separate --pmc run."]
     return lines
+
+
+TIMELINE_CLASSES = {0: "whole", 1: "direct", 2: "tree"}
+TIMELINE_PHASES = ("load_max", "exp_sum", "merge", "store")
+
+
+def item_timeline(records, clock_khz: int, part_rows: int, bins: int = 20) -> dict:
+    """Summary of one call's k_softmax_fused item trace.
+
+    ``records``: [items, 8] int64 as rg_module_set_trace writes them: ticket,
+    wall-clock stamps at the item's start, after its loads and column max,
+    after its column sums (a chunk publishes its statistics next), after the
+    segment merge and after its stores are issued, hw_id, and kind (0 whole
+    segment, 1 chunk merged directly, 2 chunk merged by tree, +4 deferred,
+    plus rows << 8); unused records are zero. Per class: items, mean rows,
+    mean phase durations (µs) and workgroup-µs. ``profile``: per 1/bins of the
+    call, the items live and merging at its midpoint. ``merge_split``, per
+    chunk class: its chunks' merge time split into waiting for the segment's
+    last chunk to publish, the chain from that publication until the
+    segment's first chunk has the merged statistics (its median per segment
+    too), and the others' later wake-ups. Segments are recovered from the
+    ticket order (a segment's chunks hold consecutive tickets, all but its
+    last of part_rows rows; two segments whose first is a multiple of
+    part_rows long are counted as one); segments with a deferred chunk are
+    left out of the split."""
+    import numpy as np
+    trace = np.asarray(records, dtype=np.int64).reshape(-1, 8)
+    trace = trace[trace[:, 1] > 0]
+    if not len(trace):
+        return {"items": 0}
+    trace = trace[np.argsort(trace[:, 0], kind="stable")]
+    us = 1000.0 / clock_khz
+    stamps = (trace[:, 1:6] - trace[:, 1].min()) * us
+    kind, rows = trace[:, 7] & 0xff, trace[:, 7] >> 8
+    cls, deferred = kind & 3, (kind & 4) != 0
+    phases = np.diff(stamps, axis=1)
+    busy = stamps[:, 4] - stamps[:, 0]
+    span = float(stamps[:, 4].max())
+    summary = {"items": int(len(trace)), "span_us": round(span, 2), "workgroup_us": round(float(busy.sum()), 1),
+               "classes": {}, "profile": []}
+    for code, name in TIMELINE_CLASSES.items():
+        mask = cls == code
+        if not mask.any():
+            continue
+        summary["classes"][name] = {
+            "items": int(mask.sum()), "deferred": int(deferred[mask].sum()),
+            "mean_rows": round(float(rows[mask].mean()), 1),
+            "phases_us": {phase: round(float(phases[mask, i].mean()), 2) for i, phase in enumerate(TIMELINE_PHASES)},
+            "workgroup_us": round(float(busy[mask].sum()), 1)}
+    for lo in np.linspace(0.0, span, bins + 1)[:-1]:
+        mid = lo + span / bins / 2
+        summary["profile"].append([int(((stamps[:, 0] <= mid) & (stamps[:, 4] > mid)).sum()),
+                                   int(((stamps[:, 2] <= mid) & (stamps[:, 3] > mid)).sum())])
+    for code in (1, 2):
+        name = TIMELINE_CLASSES[code]
+        if name not in summary["classes"]:
+            continue
+        segments, current = [], []
+        for i in np.flatnonzero(cls == code):
+            current.append(i)
+            if rows[i] < part_rows:
+                segments.append(np.array(current))
+                current = []
+        if current:
+            segments.append(np.array(current))
+        total = sibling = chain = 0.0
+        chains = []
+        for segment in segments:
+            if deferred[segment].any():
+                continue
+            published, merged = stamps[segment, 2], stamps[segment, 3]
+            last = published.max()
+            total += float((merged - published).sum())
+            sibling += float((last - published).sum())
+            chains.append(float(merged.min() - last))
+            chain += chains[-1] * len(segment)
+        if total > 0:
+            summary["classes"][name]["merge_split"] = {
+                "segments": len(chains), "merge_workgroup_us": round(total, 1),
+                "last_sibling": round(sibling / total, 3), "chain": round(chain / total, 3),
+                "wake_spread": round((total - sibling - chain) / total, 3),
+                "chain_median_us": round(float(np.median(chains)), 2)}
+    return summary
 
 
 def stats_table(stats: dict[str, dict[str, float]], limit: int = 12) -> Iterable[str]:

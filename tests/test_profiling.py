@@ -109,3 +109,38 @@ def test_csv_formats(tmp_path):
     # Rows of one dispatch (one per channel on some ROCm versions) add up.
     assert profiling.counter_per_dispatch(counters, "FETCH_SIZE")[WORKER] == {"dispatches": 2, "sum": 22.0,
                                                                               "mean": 11.0}
+
+
+def test_item_timeline_known_answers():
+    """The fused softmax's item trace reduced per class, with the merge time
+    of each chunk class split into waiting for the segment's last chunk,
+    the chain after it and the later wake-ups (ticks of a 1 MHz clock = µs)."""
+    def record(ticket, start, loaded, published, merged, end, kind, rows):
+        return [ticket, 100 + start, 100 + loaded, 100 + published, 100 + merged, 100 + end, 0, kind + (rows << 8)]
+    trace = [
+        record(0, 0, 4, 6, 20, 24, 2, 256),      # tree segment: 3 chunks, last publishes at 9
+        record(1, 0, 5, 8, 18, 23, 2, 256),
+        record(2, 1, 6, 9, 17, 21, 2, 40),
+        record(3, 2, 3, 4, 6, 8, 1, 256),        # direct segment: published 4 and 5, merged 6 and 7
+        record(4, 2, 3, 5, 7, 9, 1, 100),
+        record(5, 3, 4, 5, 30, 31, 1 + 4, 256),  # deferred: left out of the split
+        record(6, 3, 4, 6, 31, 32, 1, 10),
+        record(7, 4, 6, 8, 8, 10, 0, 200),       # whole segment
+        [0] * 8,                                  # unused record
+    ]
+    summary = profiling.item_timeline(trace, clock_khz=1000, part_rows=256, bins=4)
+    assert summary["items"] == 8 and summary["span_us"] == 32.0
+    whole = summary["classes"]["whole"]
+    assert whole["items"] == 1 and whole["phases_us"] == {"load_max": 2.0, "exp_sum": 2.0, "merge": 0.0, "store": 2.0}
+    tree = summary["classes"]["tree"]["merge_split"]
+    # merge time 14 + 10 + 8 = 32; last sibling (9-6) + (9-8) = 4; chain (17-9) x 3 = 24; spread 4
+    assert tree == {"segments": 1, "merge_workgroup_us": 32.0, "last_sibling": 0.125, "chain": 0.75,
+                    "wake_spread": 0.125, "chain_median_us": 8.0}
+    direct = summary["classes"]["direct"]
+    assert direct["items"] == 4 and direct["deferred"] == 1
+    # merge 2 + 2 = 4; last sibling 1; chain (6-5) x 2 = 2; spread 1
+    assert direct["merge_split"] == {"segments": 1, "merge_workgroup_us": 4.0, "last_sibling": 0.25, "chain": 0.5,
+                                     "wake_spread": 0.25, "chain_median_us": 1.0}
+    # Items live and merging at t = 4, 12, 20, 28.
+    assert summary["profile"] == [[8, 1], [5, 5], [5, 2], [2, 2]]
+    assert profiling.item_timeline([[0] * 8], clock_khz=1000, part_rows=256) == {"items": 0}
