@@ -524,7 +524,7 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
         !mul_ok(items_cap, (int64_t)sizeof(rg::Item), &sizes[RG_BUF_ITEMS]) ||
         !mul_ok(items_cap, 8, &sizes[RG_BUF_DEFERRED]) || !mul_ok(items_cap, 4, &sizes[RG_BUF_ARRIVE]) ||
         !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE]) || !mul_ok(item_bytes, 2, &sizes[RG_BUF_PAIRS]) ||
-        !mul_ok(stat_bytes, 2, &sizes[RG_BUF_FINAL_PAIRS]))
+        !mul_ok(rg::tree_group_rows(items_cap), (int64_t)d * 8, &sizes[RG_BUF_FINAL_PAIRS]))
       return fail(RG_E_INVALID, "fused softmax workspace bytes overflow");
     // A merge folds a segment's pairs through one buffer resource, whose
     // offsets are 32-bit: the whole pair table stays below 2 GiB.

@@ -56,10 +56,19 @@ constexpr int64_t kClassifyLarge = 16384;
 constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
 constexpr int kTreeGroup = 32;         // register-resident softmax: chunks per first-level tree group
+constexpr int kGroupRowSlot = 10;      // counters slot: final_pairs rows reserved by tree-merged segments
 constexpr int kDoneSlot = 11;          // counters slot: workgroups of the call's last kernel finished
 constexpr int kDirectDone = 64;        // up to this many active workgroups count out on kDoneSlot alone
 constexpr int32_t kStatsReady = -1;     // seg_arrive[k] once a split segment's softmax statistics are published
 constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
+
+// Rows of final_pairs (register-resident softmax): one per first-level group
+// of every segment merged by tree. Such a segment has more than kDirect of
+// the items_cap chunks, so there are at most items_cap / (kDirect + 1) of
+// them and items_cap / kTreeGroup + that many groups.
+__host__ __device__ constexpr int64_t tree_group_rows(int64_t items_cap) {
+  return items_cap / kTreeGroup + items_cap / (kDirect + 1) + 1;
+}
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
@@ -148,7 +157,7 @@ struct Item {
   int64_t start;   // first row
   int64_t seg;     // original segment id
   int32_t rows;    // rows of the item
-  int32_t k;       // split-queue position, -1 for a whole segment
+  int32_t k;       // split-queue position (a tree-merged chunk: its segment's first final_pairs row), -1 for a whole segment
   int32_t c;       // chunk index within the segment
   int32_t parts;   // chunks of the segment
 };
@@ -175,7 +184,8 @@ struct Params {
                            //      parts (worker softmax); tree items; the wave
                            //      count of a register-resident softmax; the rest
                            //      of the wave class; the split-part normalisation
-                           //      ticket; unused; done lanes finished. Then the
+                           //      ticket; final_pairs rows reserved; done lanes
+                           //      finished. Then the
                            //      worker's ticket lanes and the done lanes
                            //      (kTicketStride apart)
   int64_t* queue;          // [3, B] original segment ids per class
@@ -194,7 +204,7 @@ struct Params {
   Item* items;             // [items_cap] split chunks (register-resident softmax)
   Item* block_items;       // [B] whole segments (register-resident softmax)
   uint64_t* pairs;         // [items_cap, D] published (m, s) of each chunk
-  uint64_t* final_pairs;   // [B_split, D] merged (M, S) of long split segments
+  uint64_t* final_pairs;   // [tree_group_rows(items_cap), D] (M, S) of each group of a tree-merged segment
   int64_t spin_ticks;      // wall-clock ticks a chunk waits for its segment before deferring
   int64_t drain_ticks;     // wall-clock bound of a split part's wait for its segment's statistics
   int64_t wait_parts;      // longest segment (in chunks) whose chunks wait for each other

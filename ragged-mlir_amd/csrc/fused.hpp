@@ -13,8 +13,8 @@
 //      get the segment's merged (M, S) and write y = e * exp(m - M) / S.
 // Merging is deterministic (folds in chunk order). Up to kDirect chunks:
 // every chunk reads all published pairs itself. Longer: the last chunk of
-// each group of kGroup folds the group, the last group folds the groups and
-// publishes (M, S), and those segments are dequeued first. A chunk waits
+// each group of kGroup folds the group and publishes it, every chunk folds
+// the group results, and those segments are dequeued first. A chunk waits
 // for its segment with a bounded spin: since items are dequeued in order
 // and a workgroup holds an unstarted ticket only when it cannot wait or all
 // chunks of its segment are handed out, every chunk it waits for is started
@@ -214,8 +214,9 @@ __device__ __forceinline__ void block_allreduce(float (&v)[VEC], int lpr, int fe
 // Statistics shared between workgroups travel only through agent-scope
 // atomic stores and loads (coherent across the XCDs' L2 caches), so no
 // L2-wide writeback or invalidate is needed. Each (m, s) pair of a feature is
-// one 64-bit store; k_classify fills every slot with a sentinel first (s bits
-// 0x7F800001, a signalling NaN, which f32 arithmetic never produces), so a
+// one 64-bit store; k_init fills every slot (chunk pairs and group rows)
+// with a sentinel first (s bits 0x7F800001, a signalling NaN, which f32
+// arithmetic never produces), so a
 // reader polls the data itself instead of a separate flag. A publisher that
 // bumps a counter waits for its stores to complete (s_waitcnt vmcnt(0))
 // before the barrier after which one thread updates the counter.
@@ -378,21 +379,21 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
   }
 }
 
-// Counter-based tree merge of a long segment: the last chunk of each group
-// folds the group into slot gfirst (into final_pairs[k] when the segment is
-// one group), the last group folds the groups into final_pairs[k]. Never
-// waits: every slot a fold reads was published (stores complete, then the
-// barrier) before the counter increment that made this workgroup the last.
-// The group fold replaces chunk gfirst's own pair, so a deferred chunk takes
-// its own column max from its rows, not from its pair slot.
-__device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t k, int* flag_s,
+// Counter-based first level of a long segment's merge: the last chunk of
+// each group of kGroup folds the group and publishes it in the segment's
+// row gbase + group of final_pairs (sentinel-filled, like every pair slot).
+// The fold never waits: every slot it reads was published (stores complete,
+// then the barrier) before the counter increment that made this workgroup
+// the last. The segment's chunks then fold its groups' rows directly, as a
+// directly merged segment folds its chunks' pairs: no second counter level,
+// whose store, atomic, fold and store again would sit on every chunk's wait.
+__device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t gbase, int* flag_s,
                            float* lds_m, float* lds_s, uint64_t* stage) {
   const int t = local_tid();
   const int d = p.d;
   const int64_t group = (slot - first) / kGroup;
   const int64_t gfirst = first + group * kGroup;
   const int64_t gsize = parts - group * kGroup < kGroup ? parts - group * kGroup : kGroup;
-  const int64_t groups = (parts + kGroup - 1) / kGroup;
   // Every read of *flag_s is followed by a barrier before its next write.
   wait_stores();
   __syncthreads();
@@ -402,18 +403,7 @@ __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t
   __syncthreads();
   if (!last_in_group) return;
   (void)fold_block(p.pairs + gfirst * d, gsize, 1, d, lds_m, lds_s, stage);
-  uint64_t* dest = groups == 1 ? p.final_pairs + k * d : p.pairs + gfirst * d;
-  for (int f = t; f < d; f += kBlock) store_pair(dest + f, lds_m[f], lds_s[f]);
-  if (groups == 1) return;
-  wait_stores();
-  __syncthreads();
-  if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == groups - 1;
-  __syncthreads();
-  const bool last_group = *flag_s != 0;
-  __syncthreads();
-  if (!last_group) return;
-  (void)fold_block(p.pairs + first * d, groups, kGroup, d, lds_m, lds_s, stage);
-  for (int f = t; f < d; f += kBlock) store_pair(p.final_pairs + k * d + f, lds_m[f], lds_s[f]);
+  for (int f = t; f < d; f += kBlock) store_pair(p.final_pairs + (gbase + group) * d + f, lds_m[f], lds_s[f]);
 }
 
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
@@ -643,8 +633,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         const int64_t* tickets = p.counters + 4;
         const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, tickets, last_ticket,
                                               lds, lds_s, stage)
-                                  : wait_fold(p.final_pairs + it.k * d, 1, p.d, p.spin_ticks, tickets, last_ticket,
-                                              lds, lds_s, stage);
+                                  : wait_fold(p.final_pairs + it.k * d, (parts + kGroup - 1) / kGroup, p.d,
+                                              p.spin_ticks, tickets, last_ticket, lds, lds_s, stage);
         defer = !ready;
         // Same thread wrote lds[f] / lds_s[f] in the fold: no barrier needed.
         if (ready) {
@@ -758,8 +748,7 @@ __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
   for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
     const int64_t slot = p.deferred[i];
     const Item it = p.items[slot];
-    // The chunk's own column max, from its rows (the tree merge may have
-    // replaced its published pair by its group's): IEEE maximum is exact in
+    // The chunk's own column max, from its rows: IEEE maximum is exact in
     // any order, so it equals the register path's.
     State<OP_MAX> own[VEC];
     init_all<OP_MAX, VEC>(own);
@@ -767,7 +756,7 @@ __global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
     block_reduce<OP_MAX, VEC>(own, g.lpr, g.feat_lane, lds_m);
     // Every pair is published once k_softmax_fused has finished.
     if (it.parts <= kDirect) (void)fold_block(p.pairs + (slot - it.c) * p.d, it.parts, 1, p.d, lds_m, lds_s, stage);
-    else (void)fold_block(p.final_pairs + it.k * p.d, 1, 1, p.d, lds_m, lds_s, stage);
+    else (void)fold_block(p.final_pairs + it.k * p.d, (it.parts + kGroup - 1) / kGroup, 1, p.d, lds_m, lds_s, stage);
     __syncthreads();
     if (g.active) {
       float ref[VEC], factor[VEC];

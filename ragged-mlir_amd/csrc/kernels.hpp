@@ -482,7 +482,7 @@ __global__ __launch_bounds__(kBlock) void k_init(Params p) {
     // 256-byte aligned), an odd last slot alone.
     const uint64_t sentinel = (uint64_t)kSentinel << 32;
     const ulonglong2 two = {sentinel, sentinel};
-    const int64_t slots = p.items_cap * p.d, final_slots = p.b_split * p.d;
+    const int64_t slots = p.items_cap * p.d, final_slots = tree_group_rows(p.items_cap) * p.d;
     ulonglong2* pairs2 = reinterpret_cast<ulonglong2*>(p.pairs);
     ulonglong2* final2 = reinterpret_cast<ulonglong2*>(p.final_pairs);
     for (int64_t i = tid; i < slots / 2; i += threads) pairs2[i] = two;
@@ -564,14 +564,17 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
     // register-resident softmax (p.items set) takes segments of more than
     // kDirect chunks from the top of the item array, so they are dequeued
     // first, while every workgroup of the grid is still free to hold one.
-    long long first = 0, parts = 0;
+    long long first = 0, parts = 0, gbase = 0;
     bool fits = true;
     if (mine && pos < p.b_split) {
       parts = (length + p.part_rows - 1) / p.part_rows;
       if (p.items && parts > kDirect) {
         const long long above = (long long)atomicAdd((unsigned long long*)(p.counters + 6), (unsigned long long)parts);
         first = (long long)p.items_cap - above - parts;
-        fits = first >= 0;
+        // The segment's rows of final_pairs, one per group of kTreeGroup.
+        const long long groups = (parts + kTreeGroup - 1) / kTreeGroup;
+        gbase = (long long)atomicAdd((unsigned long long*)(p.counters + kGroupRowSlot), (unsigned long long)groups);
+        fits = first >= 0 && gbase + groups <= tree_group_rows(p.items_cap);
       } else {
         first = (long long)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
         fits = first + parts <= p.items_cap;
@@ -604,7 +607,8 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
         const long long f = lane_value((int64_t)first, src), count = lane_value((int64_t)parts, src);
         const int64_t lo = f > 0 ? f : 0;
         const int64_t last = f + count < p.items_cap ? f + count : p.items_cap;
-        const long long k = lane_value((int64_t)pos, src), seg = lane_value((int64_t)s, src);
+        // A tree-merged chunk's k: its segment's first row of final_pairs.
+        const long long k = lane_value((int64_t)gbase, src), seg = lane_value((int64_t)s, src);
         const long long seg_start = lane_value((int64_t)start, src);
         const long long seg_rows = lane_value((int64_t)length, src);
         const bool whole = lane_value((int)fits, src) != 0;
