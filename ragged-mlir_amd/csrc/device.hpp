@@ -55,7 +55,7 @@ constexpr int kClassifyWaves = kClassifyBlock / kWave;
 constexpr int64_t kClassifyLarge = 16384;
 constexpr int kTicketStride = 32;
 constexpr int kDirect = 16;            // register-resident softmax: chunks merged by all-read
-constexpr int kTreeGroup = 32;         // register-resident softmax: chunks per first-level tree group
+constexpr int kTreeGroup = 16;         // register-resident softmax: chunks per first-level tree group
 constexpr int kGroupRowSlot = 10;      // counters slot: final_pairs rows reserved by tree-merged segments
 constexpr int kDoneSlot = 11;          // counters slot: workgroups of the call's last kernel finished
 constexpr int kDirectDone = 64;        // up to this many active workgroups count out on kDoneSlot alone
