@@ -48,10 +48,10 @@ enum rg_index { RG_I32 = 0, RG_I64 = 1 };
  * alone_rows or t_wave is 0. */
 enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1, RG_SHORT_SEGMENTS = 2 };
 
-/* Kernel roles, in launch order of the classified schedule. */
+/* Kernel roles (a plan lists its launches in submission order). */
 enum rg_role {
-  RG_ROLE_INIT = 0,            /* register-resident softmax only: pair slots; otherwise
-                                  k_classify initialises what a call uses */
+  RG_ROLE_INIT = 0,            /* register-resident softmax only, after RG_ROLE_CLASSIFY: the statistics
+                                  slots its merges poll; otherwise k_classify initialises what a call uses */
   RG_ROLE_CLASSIFY = 1,
   RG_ROLE_WAVE = 2,            /* not launched: the wave class runs inside RG_ROLE_WORKER */
   RG_ROLE_BLOCK = 3,           /* not launched: the block class runs inside RG_ROLE_WORKER */

@@ -543,15 +543,14 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   }
   plan->workspace_bytes = (uint64_t)end;
 
-  if (module->fused) {
-    // Grid-stride fill of every pair slot (8 per thread).
-    add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, items_cap * d / (rg::kBlock * 8))), 1);
-  }
   const int classify_block = b >= rg::kClassifyLarge ? rg::kClassifyBlock : rg::kBlock;
   add_launch(RG_ROLE_CLASSIFY, (b + classify_block - 1) / classify_block, 1, classify_block);
   if (module->fused) {
-    // The block and split classes held in registers; then the deferred
-    // chunks and the wave class, in the streaming worker's batches.
+    // Grid-stride fill of the slots the call's merges poll (sized for the
+    // most: every item's pair, 8 per thread); the block and split classes
+    // held in registers; then the deferred chunks and the wave class, in the
+    // streaming worker's batches.
+    add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, items_cap * d / (rg::kBlock * 8))), 1);
     add_launch(RG_ROLE_FUSED, std::min(module->resident[RG_ROLE_FUSED], b + items_cap), 1);
     add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], std::max(items_cap, stride_grid)), 1);
     return RG_OK;

@@ -460,37 +460,32 @@ __device__ __forceinline__ void reset_counters(const Params& p) {
 #ifdef RG_PROLOGUE_KERNELS
 // Defined in exactly one translation unit (kernels_common.hip).
 
-// Register-resident softmax only (the streaming worker's calls need no
-// separate init): zero the class counters, the debug visit counts and the
-// merge counters, and fill every statistics pair slot with the unpublished
-// sentinel (grid-stride, coalesced; the polling merge needs the whole array
-// ready before any chunk publishes).
+// Register-resident softmax, after k_classify: fill the statistics slots
+// this call's merges poll with the unpublished sentinel -- the pairs of the
+// directly merged chunks (the bottom counters[3] items) and the group rows
+// of the tree-merged segments (counters[kGroupRowSlot]) -- and zero the tree
+// chunks' group arrival counters (the top counters[6] items). A tree chunk's
+// own pair is read only after its group's counter says it is published, so
+// it needs no sentinel. Everything else a call uses k_classify initialises,
+// or the previous call's last workgroup returned to zero (the counters).
+// Grid-stride, 16-byte stores where the span allows.
 __global__ __launch_bounds__(kBlock) void k_init(Params p) {
   const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const int64_t threads = (int64_t)gridDim.x * kBlock;
-  // Every class counter slot (the first kTicketStride) and every ticket lane.
-  if (tid < kTicketStride) p.counters[tid] = 0;
-  if (tid < 2 * kTicketLanes) p.counters[kTicketStride * (1 + tid)] = 0;   // ticket and done lanes
-  if (p.visits) {
-    for (int64_t s = tid; s < p.b; s += threads) p.visits[s] = 0;
-  }
-  if (p.seg_arrive) {
-    for (int64_t i = tid; i < p.b_split; i += threads) p.seg_arrive[i] = 0;
-  }
-  if (p.pairs) {
-    // Pair slots in 16-byte stores (two slots each; both arrays start
-    // 256-byte aligned), an odd last slot alone.
-    const uint64_t sentinel = (uint64_t)kSentinel << 32;
-    const ulonglong2 two = {sentinel, sentinel};
-    const int64_t slots = p.items_cap * p.d, final_slots = tree_group_rows(p.items_cap) * p.d;
-    ulonglong2* pairs2 = reinterpret_cast<ulonglong2*>(p.pairs);
-    ulonglong2* final2 = reinterpret_cast<ulonglong2*>(p.final_pairs);
-    for (int64_t i = tid; i < slots / 2; i += threads) pairs2[i] = two;
-    for (int64_t i = tid; i < final_slots / 2; i += threads) final2[i] = two;
-    if (tid == 0 && (slots & 1)) p.pairs[slots - 1] = sentinel;
-    if (tid == 0 && (final_slots & 1)) p.final_pairs[final_slots - 1] = sentinel;
-    for (int64_t i = tid; i < p.items_cap; i += threads) p.arrive[i] = 0;
-  }
+  const int64_t n_tree = p.counters[6] < p.items_cap ? p.counters[6] : p.items_cap;
+  const int64_t n_direct = p.counters[3] < p.items_cap - n_tree ? p.counters[3] : p.items_cap - n_tree;
+  const int64_t rows_cap = tree_group_rows(p.items_cap);
+  const int64_t rows = p.counters[kGroupRowSlot] < rows_cap ? p.counters[kGroupRowSlot] : rows_cap;
+  const uint64_t sentinel = (uint64_t)kSentinel << 32;
+  const ulonglong2 two = {sentinel, sentinel};
+  auto fill = [&](uint64_t* slots, int64_t count) {   // slots: 256-byte aligned
+    ulonglong2* pairs2 = reinterpret_cast<ulonglong2*>(slots);
+    for (int64_t i = tid; i < count / 2; i += threads) pairs2[i] = two;
+    if (tid == 0 && (count & 1)) slots[count - 1] = sentinel;
+  };
+  fill(p.pairs, n_direct * p.d);
+  fill(p.final_pairs, rows * p.d);
+  for (int64_t i = p.items_cap - n_tree + tid; i < p.items_cap; i += threads) p.arrive[i] = 0;
 }
 
 // Bin segments: wave (L <= t_wave), block (L <= t_block), split (longer).

@@ -37,15 +37,16 @@ def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> 
     """Role names in launch order. The classified schedule runs classify
     (which also initialises the per-segment state of the call) and one
     worker over the wave, block and split classes (a softmax's worker also
-    normalises its split parts); with ``fused`` a softmax runs its
+    normalises its split parts); with ``fused`` a softmax runs classify, an
+    init pass over the statistics slots the call's merges poll, its
     register-resident worker, then a pass over the deferred chunks and the
-    wave class, after an init pass over its pair slots. The last kernel's
-    last workgroup returns the workspace's counters to zero."""
+    wave class. The last kernel's last workgroup returns the workspace's
+    counters to zero."""
     phase = _phase(spec.op)
     if classes == ["block"] and spec.strategy == "naive":
         return [phase]
     if fused:
-        return ["init", "classify", "fused_online", "deferred_online"]
+        return ["classify", "init", "fused_online", "deferred_online"]
     roles = ["classify"]
     # One persistent worker drains every class; the reference's per-class
     # chains, split combine and (softmax) split normalisation run inside it.
