@@ -44,7 +44,7 @@ def test_suites_are_fixed_and_disjoint():
     assert suites["train"] == calibrate.suite("train")
     assert {name: len(cases) for name, cases in suites.items()} == {
         "train": 330, "train_dense": 420, "heldout": 150, "heldout2": 150, "heldout3": 150, "heldout4": 150,
-        "heldout5": 150, "heldout6": 150}
+        "heldout5": 150, "heldout6": 150, "heldout7": 150}
     held = [name for name in suites if name.startswith("heldout")]
     pairs = [(a, b) for a in held for b in held if a < b] + [(t, h) for t in ("train", "train_dense") for h in held]
     for a, b in pairs:
@@ -53,19 +53,22 @@ def test_suites_are_fixed_and_disjoint():
         assert {c.key for c in suites[a]}.isdisjoint({c.key for c in suites[b]}), (a, b)
     heldout2 = suites["heldout2"]
     # Some working sets (rows read plus rows written) of most held-out suites
-    # (the shipped model's heldout6 among them) exceed the 256 MiB Infinity Cache.
-    for suite in (suites[name] for name in ("heldout", "heldout2", "heldout3", "heldout5", "heldout6")):
+    # (the shipped model's heldout7 among them) exceed the 256 MiB Infinity Cache.
+    for suite in (suites[name] for name in ("heldout", "heldout2", "heldout3", "heldout5", "heldout6", "heldout7")):
         assert any(c.n * c.d * c.element_bytes * (2 if c.op == "softmax" else 1) > 256 << 20 for c in suite)
     # heldout2's shapes: fixed by its seed (a change of the suite would
     # silently unfreeze it).
     assert [c.key for c in heldout2[:3]] == FROZEN_HELDOUT2_HEAD
     assert [c.key for c in suites["heldout6"][:3]] == FROZEN_HELDOUT6_HEAD
+    assert [c.key for c in suites["heldout7"][:3]] == FROZEN_HELDOUT7_HEAD
 
 
 FROZEN_HELDOUT2_HEAD = ["sum-f32-d3-n262144-b8192-long_tail-s9000", "sum-f32-d3-n262144-b8192-burst-s9001",
                         "sum-f32-d3-n2097152-b8192-uniform-s9002"]
 FROZEN_HELDOUT6_HEAD = ["sum-f32-d13-n181484-b448-long_tail-s25000", "sum-f32-d13-n181484-b57344-uniform-s25001",
                         "sum-f32-d13-n181484-b57344-bimodal-s25002"]
+FROZEN_HELDOUT7_HEAD = ["sum-f32-d15-n192238-b320-burst-s29000", "sum-f32-d15-n192238-b320-exponential-s29001",
+                        "sum-f32-d15-n192238-b28672-burst-s29002"]
 
 
 @pytest.mark.parametrize("op", ["sum", "max", "softmax"])
