@@ -148,15 +148,15 @@ def test_evaluate_counts_within_three_percent():
     assert len(calibrate.evaluate(bad, records)["misses"]) == expected
 
 
-TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5")
+TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5", "heldout6")
 
 
 def test_shipped_model_records_its_heldout_scores():
     """The committed cost model is the fit of the committed MI355X
-    measurements of every suite but heldout6, pooled (refitting reproduces
+    measurements of every suite but heldout7, pooled (refitting reproduces
     its coefficients and margins), all measured with the library whose
     sha256 it records; its choices, as run(select="auto") makes them, are
-    scored on heldout6 (frozen before the fit, disjoint shapes, scored once)
+    scored on heldout7 (frozen before the fit, disjoint shapes, scored once)
     warm and cold exactly as recorded. Every measured case passed the
     sampled correctness gate."""
     base = Path(calibrate.__file__).with_name("calibration")
@@ -168,10 +168,10 @@ def test_shipped_model_records_its_heldout_scores():
     model = CostModel.load()
     shas = {r["library_sha256"] for records in files.values() for r in records}
     assert shas == {model.calibration["library_sha256"]}
-    heldout = files["heldout6"]
+    heldout = files["heldout7"]
     warm, cold = calibrate.evaluate(model, heldout), calibrate.evaluate(model, heldout, cold=True)
     assert warm["cases"] == cold["cases"] == 150
-    assert model.calibration["heldout_file"] == "heldout6.jsonl"
+    assert model.calibration["heldout_file"] == "heldout7.jsonl"
     assert model.calibration["train_file"] == " + ".join(f"{name}.jsonl" for name in TRAIN_SUITES)
     assert model.calibration["heldout_within_3pct"] == warm["share"]
     assert model.calibration["heldout_within_3pct_cold"] == cold["share"]
@@ -189,7 +189,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     held-out share; the CLI writes the refit and prints the report."""
     directory = Path(calibrate.__file__).with_name("calibration")
     train = [r for name in TRAIN_SUITES for r in calibrate.load(directory / f"{name}.jsonl")]
-    heldout = calibrate.load(directory / "heldout6.jsonl")
+    heldout = calibrate.load(directory / "heldout7.jsonl")
     shipped = CostModel.load()
     data, report = calibrate.transfer(train, heldout, shipped)
     assert data["coefficients"] == json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())[
@@ -201,7 +201,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     out = tmp_path / "refit.json"
     pooled = tmp_path / "train_pooled.jsonl"
     pooled.write_text("".join(json.dumps(record) + "\n" for record in train))
-    assert calibrate.main(["transfer", str(pooled), str(directory / "heldout6.jsonl"), "--out", str(out)]) == 0
+    assert calibrate.main(["transfer", str(pooled), str(directory / "heldout7.jsonl"), "--out", str(out)]) == 0
     assert json.loads(out.read_text())["coefficients"] == data["coefficients"]
 
 
