@@ -93,17 +93,19 @@ def _grid(ds, elements, segments, seed0, count, seed_grid):
 
 
 SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5", "heldout6",
-          "heldout7")
+          "heldout7", "heldout8")
 
 
 def suite(name: str) -> list[Case]:
     """The fixed shape suites. The held-out suites share no feature width,
     size or segment count with either train suite or with each other;
-    heldout, heldout2, heldout3, heldout5, heldout6 and heldout7 reach beyond
-    the 256 MiB Infinity Cache (working sets up to 512, 384, 320, 384, 576 and
-    352 MiB). Each was frozen before the fit it scores and scored once for it:
-    ``heldout7`` for the shipped model (fitted on every other suite pooled:
-    their measurements on the shipped library); ``heldout6`` for the same
+    heldout, heldout2, heldout3, heldout5, heldout6, heldout7 and heldout8
+    reach beyond the 256 MiB Infinity Cache (working sets up to 512, 384, 320,
+    384, 576, 352 and 416 MiB). Each was frozen before the fit it scores and scored once for it:
+    ``heldout8`` for the shipped model (fitted on every other suite pooled:
+    their measurements on the shipped library); ``heldout7`` for the same
+    model form fitted on the eight suites before it, measured on the build
+    before the register-resident softmax's wave-priority change; ``heldout6`` for the same
     model form fitted on the seven suites before it, measured on the library
     build before the register-resident softmax's merge changes (tree groups
     of 16 chunks, sentinel fill after classification); ``heldout5`` for a fit on
@@ -140,6 +142,9 @@ def suite(name: str) -> list[Case]:
     if name == "heldout7":
         return _grid(ds=(15, 26, 44, 88, 224), elements=(11 << 18, 11 << 21, 11 << 22),
                      segments=(320, 7168, 28672), seed0=29000, count=150, seed_grid=71)
+    if name == "heldout8":
+        return _grid(ds=(17, 30, 52, 104, 208), elements=(13 << 18, 13 << 21, 13 << 22),
+                     segments=(576, 6656, 36864), seed0=33000, count=150, seed_grid=73)
     raise ValueError(f"suite must be one of {SUITES}")
 
 

@@ -44,7 +44,7 @@ def test_suites_are_fixed_and_disjoint():
     assert suites["train"] == calibrate.suite("train")
     assert {name: len(cases) for name, cases in suites.items()} == {
         "train": 330, "train_dense": 420, "heldout": 150, "heldout2": 150, "heldout3": 150, "heldout4": 150,
-        "heldout5": 150, "heldout6": 150, "heldout7": 150}
+        "heldout5": 150, "heldout6": 150, "heldout7": 150, "heldout8": 150}
     held = [name for name in suites if name.startswith("heldout")]
     pairs = [(a, b) for a in held for b in held if a < b] + [(t, h) for t in ("train", "train_dense") for h in held]
     for a, b in pairs:
@@ -53,14 +53,16 @@ def test_suites_are_fixed_and_disjoint():
         assert {c.key for c in suites[a]}.isdisjoint({c.key for c in suites[b]}), (a, b)
     heldout2 = suites["heldout2"]
     # Some working sets (rows read plus rows written) of most held-out suites
-    # (the shipped model's heldout7 among them) exceed the 256 MiB Infinity Cache.
-    for suite in (suites[name] for name in ("heldout", "heldout2", "heldout3", "heldout5", "heldout6", "heldout7")):
+    # (the shipped model's heldout8 among them) exceed the 256 MiB Infinity Cache.
+    for suite in (suites[name] for name in ("heldout", "heldout2", "heldout3", "heldout5", "heldout6", "heldout7",
+                                            "heldout8")):
         assert any(c.n * c.d * c.element_bytes * (2 if c.op == "softmax" else 1) > 256 << 20 for c in suite)
     # heldout2's shapes: fixed by its seed (a change of the suite would
     # silently unfreeze it).
     assert [c.key for c in heldout2[:3]] == FROZEN_HELDOUT2_HEAD
     assert [c.key for c in suites["heldout6"][:3]] == FROZEN_HELDOUT6_HEAD
     assert [c.key for c in suites["heldout7"][:3]] == FROZEN_HELDOUT7_HEAD
+    assert [c.key for c in suites["heldout8"][:3]] == FROZEN_HELDOUT8_HEAD
 
 
 FROZEN_HELDOUT2_HEAD = ["sum-f32-d3-n262144-b8192-long_tail-s9000", "sum-f32-d3-n262144-b8192-burst-s9001",
@@ -69,6 +71,8 @@ FROZEN_HELDOUT6_HEAD = ["sum-f32-d13-n181484-b448-long_tail-s25000", "sum-f32-d1
                         "sum-f32-d13-n181484-b57344-bimodal-s25002"]
 FROZEN_HELDOUT7_HEAD = ["sum-f32-d15-n192238-b320-burst-s29000", "sum-f32-d15-n192238-b320-exponential-s29001",
                         "sum-f32-d15-n192238-b28672-burst-s29002"]
+
+FROZEN_HELDOUT8_HEAD = ["sum-f32-d17-n200463-b6656-bimodal-s33000", "sum-f32-d17-n1603704-b576-uniform-s33001", "sum-f32-d17-n1603704-b576-exponential-s33002"]
 
 
 @pytest.mark.parametrize("op", ["sum", "max", "softmax"])
@@ -148,15 +152,16 @@ def test_evaluate_counts_within_three_percent():
     assert len(calibrate.evaluate(bad, records)["misses"]) == expected
 
 
-TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5", "heldout6")
+TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5", "heldout6",
+                "heldout7")
 
 
 def test_shipped_model_records_its_heldout_scores():
     """The committed cost model is the fit of the committed MI355X
-    measurements of every suite but heldout7, pooled (refitting reproduces
+    measurements of every suite but heldout8, pooled (refitting reproduces
     its coefficients and margins), all measured with the library whose
     sha256 it records; its choices, as run(select="auto") makes them, are
-    scored on heldout7 (frozen before the fit, disjoint shapes, scored once)
+    scored on heldout8 (frozen before the fit, disjoint shapes, scored once)
     warm and cold exactly as recorded. Every measured case passed the
     sampled correctness gate."""
     base = Path(calibrate.__file__).with_name("calibration")
@@ -168,10 +173,10 @@ def test_shipped_model_records_its_heldout_scores():
     model = CostModel.load()
     shas = {r["library_sha256"] for records in files.values() for r in records}
     assert shas == {model.calibration["library_sha256"]}
-    heldout = files["heldout7"]
+    heldout = files["heldout8"]
     warm, cold = calibrate.evaluate(model, heldout), calibrate.evaluate(model, heldout, cold=True)
     assert warm["cases"] == cold["cases"] == 150
-    assert model.calibration["heldout_file"] == "heldout7.jsonl"
+    assert model.calibration["heldout_file"] == "heldout8.jsonl"
     assert model.calibration["train_file"] == " + ".join(f"{name}.jsonl" for name in TRAIN_SUITES)
     assert model.calibration["heldout_within_3pct"] == warm["share"]
     assert model.calibration["heldout_within_3pct_cold"] == cold["share"]
@@ -189,7 +194,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     held-out share; the CLI writes the refit and prints the report."""
     directory = Path(calibrate.__file__).with_name("calibration")
     train = [r for name in TRAIN_SUITES for r in calibrate.load(directory / f"{name}.jsonl")]
-    heldout = calibrate.load(directory / "heldout7.jsonl")
+    heldout = calibrate.load(directory / "heldout8.jsonl")
     shipped = CostModel.load()
     data, report = calibrate.transfer(train, heldout, shipped)
     assert data["coefficients"] == json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())[
@@ -201,7 +206,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     out = tmp_path / "refit.json"
     pooled = tmp_path / "train_pooled.jsonl"
     pooled.write_text("".join(json.dumps(record) + "\n" for record in train))
-    assert calibrate.main(["transfer", str(pooled), str(directory / "heldout7.jsonl"), "--out", str(out)]) == 0
+    assert calibrate.main(["transfer", str(pooled), str(directory / "heldout8.jsonl"), "--out", str(out)]) == 0
     assert json.loads(out.read_text())["coefficients"] == data["coefficients"]
 
 
