@@ -214,18 +214,14 @@ def cpu_baselines(op, dtype, values_f32, offsets, algorithmic_bytes: int) -> lis
 def role_bytes(role: str, op: str, lengths: np.ndarray, d: int, element: int, t_wave: int, t_block: int,
                offset_bytes: int = 8) -> int:
     """Algorithmic bytes of the rows one kernel role owns. The
-    register-resident softmax ("fused") reads and writes every row of the
-    segments longer than t_wave once; after it "deferred" does the same for
-    the wave class (its re-read of deferred chunks is not algorithmic);
+    register-resident softmax ("fused") reads and writes every row once: the
+    segments longer than t_wave held in registers, then the wave class in
+    batches (a re-read of a chunk that stopped waiting is not algorithmic);
     "classify" reads the offsets."""
     if role == "fused":
-        return 2 * int(lengths[lengths > t_wave].sum()) * d * element
-    if role == "deferred":
-        return 2 * int(lengths[lengths <= t_wave].sum()) * d * element
+        return 2 * int(lengths.sum()) * d * element
     if role == "classify":
         return (len(lengths) + 1) * offset_bytes
-    if role == "init":
-        return 0
     if role == "worker":
         # The classified worker reads every row once and writes every
         # reduction result, or every softmax row (split segments' rows after

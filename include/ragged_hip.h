@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define RG_ABI_VERSION 2
+#define RG_ABI_VERSION 3
 
 enum rg_status {
   RG_OK = 0,
@@ -50,8 +50,7 @@ enum rg_schedule { RG_CLASSIFIED = 0, RG_BLOCK_PER_SEGMENT = 1, RG_SHORT_SEGMENT
 
 /* Kernel roles (a plan lists its launches in submission order). */
 enum rg_role {
-  RG_ROLE_INIT = 0,            /* register-resident softmax only, after RG_ROLE_CLASSIFY: the statistics
-                                  slots its merges poll; otherwise k_classify initialises what a call uses */
+  RG_ROLE_INIT = 0,            /* not launched: k_classify initialises what a call uses */
   RG_ROLE_CLASSIFY = 1,
   RG_ROLE_WAVE = 2,            /* not launched: the wave class runs inside RG_ROLE_WORKER */
   RG_ROLE_BLOCK = 3,           /* not launched: the block class runs inside RG_ROLE_WORKER */
@@ -59,9 +58,9 @@ enum rg_role {
   RG_ROLE_SPLIT_COMBINE = 5,   /* not launched: the last part of a segment combines, inside RG_ROLE_WORKER */
   RG_ROLE_SPLIT_NORMALIZE = 6, /* not launched: the classified worker normalises split parts */
   RG_ROLE_NAIVE = 7,           /* block-per-segment schedule */
-  RG_ROLE_FUSED = 8,           /* softmax: register-resident worker over all block/split items */
-  RG_ROLE_DEFERRED = 9,        /* softmax: re-read pass for chunks that stopped waiting, then the
-                                  register-resident softmax's wave class */
+  RG_ROLE_FUSED = 8,           /* softmax: register-resident worker over all block/split items, then the
+                                  wave class and the chunks that stopped waiting (re-read) */
+  RG_ROLE_DEFERRED = 9,        /* not launched: RG_ROLE_FUSED drains its deferred chunks itself */
   RG_ROLE_WORKER = 10,         /* persistent worker over the wave, block and split queues */
   RG_ROLE_COUNT = 11
 };
@@ -130,11 +129,18 @@ enum rg_buffer {
                                (register-resident softmax chunks, or worker softmax split
                                parts), 6 tree items; 7 slot 0's count for a register-resident
                                softmax (whose slot 0 stays 0); 8 the rest of the wave class;
-                               9 softmax split-part normalisation ticket; 10 unused; 11 done
-                               lanes finished (of the call's last kernel); then 16 ticket
-                               counters of the classified worker and 16 done lanes, 256 bytes
-                               apart from byte 256 (8448 bytes in all). All zero before a
-                               call; the call's last workgroup leaves them zero. */
+                               9 softmax split-part normalisation ticket; 10 final_pairs rows
+                               reserved (register-resident softmax); 11 done lanes finished
+                               (of the call's last kernel); 12 the fused softmax arena's state
+                               (0: the workspace is as allocated, all zero; 1: unknown, another
+                               plan's buffers overlap it; v >= 2: its first v - 2 bytes are zero
+                               but for the byte ranges [14, 15), [16, 17), [18, 19) hold: the
+                               pairs and group rows the last call published, which the next
+                               call's classification zeroes); 13 deferred chunks claimed; then
+                               16 ticket counters of the classified worker and 16 done lanes,
+                               256 bytes apart from byte 256 (8448 bytes in all). All zero
+                               before a call but slots 12 and 14-19; the call's last workgroup
+                               leaves them so. */
   RG_BUF_QUEUE = 1,         /* i64[3, B] original segment ids per class; the wave class holds
                                its segments of at most alone_rows rows from the front and the
                                others from the back */
@@ -145,16 +151,22 @@ enum rg_buffer {
   RG_BUF_STATS_MAX = 6,     /* f32[B_split, D] (softmax) */
   RG_BUF_STATS_SUM = 7,     /* f32[B_split, D] (softmax) */
   RG_BUF_VISITS = 8,        /* i32[B] (debug_visits) */
-  RG_BUF_DEFERRED = 9,      /* i64[items_cap] chunks left to the re-read pass (fused softmax);
-                               i64[items_cap * feature tiles] split parts left to the worker's
-                               last workgroup (worker softmax) */
-  RG_BUF_ARRIVE = 10,       /* i32[items_cap] chunk arrivals per 32-chunk group (fused softmax) */
-  RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] part (fused softmax: group) arrivals per split segment */
+  RG_BUF_DEFERRED = 9,      /* i64[items_cap] 1 + item of each chunk left to the drain, 0 while
+                               unwritten (fused softmax); i64[items_cap * feature tiles] split
+                               parts left to the worker's last workgroup (worker softmax) */
+  RG_BUF_ARRIVE = 10,       /* i32[items_cap] chunk arrivals per 16-chunk group and readers of
+                               each segment's merged statistics (fused softmax) */
+  RG_BUF_SEG_ARRIVE = 11,   /* i32[B_split] part arrivals per split segment (worker) */
   RG_BUF_ITEMS = 12,        /* 32-byte descriptors [items_cap] of split chunks (fused softmax) */
   RG_BUF_BLOCK_ITEMS = 13,  /* 32-byte descriptors [B] of whole segments (fused softmax) */
   RG_BUF_PAIRS = 14,        /* u64[items_cap, D] published (max, sum) of each chunk (fused softmax) */
-  RG_BUF_FINAL_PAIRS = 15   /* u64[B_split, D] merged (max, sum) of long segments (fused softmax) */
+  RG_BUF_FINAL_PAIRS = 15   /* u64[rows, D] merged (max, sum) of each 16-chunk group of a long
+                               segment (fused softmax) */
 };
+/* Buffers are laid out at 256-byte aligned offsets: the counters at 0, then
+ * the fused softmax's arena (pairs, final pairs, arrive, deferred: the slots
+ * that hold zero between its calls) at the same offset in every plan, then
+ * the rest. */
 
 typedef struct rg_module rg_module;
 
@@ -201,41 +213,58 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
  *
  * Workspace contract: zero-filled before its first call. Every call
  * initialises the per-segment state it uses and its last workgroup returns
- * the workspace's counters to zero, so calls in order on one stream reuse it
- * with no clearing (a failed rg_run may leave it dirty: zero it again). A
+ * the workspace's counters to zero; a fused softmax call also records which
+ * bytes of its arena it left nonzero (counters slots 12, 14-19), and the
+ * next call's classification zeroes those and whatever part of its plan's
+ * arena a call of another plan overwrote.
+ * So calls in order on one stream reuse a workspace with no clearing, across
+ * plans and modules (a failed rg_run may leave it dirty: zero it again). A
  * module with debug_visits keeps its counters for inspection instead: give
  * each of its calls a zeroed workspace. */
 int rg_run(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
            void* out, const float* mask, void* workspace, uint64_t workspace_bytes, void* stream);
 
-/* Size of the static workspace rg_run_static uses on each device (64 MiB). */
+/* Size of the static workspace rg_run_static uses on each device (64 MiB
+ * unless the library is built with another -DRG_STATIC_WORKSPACE_BYTES). */
+#ifndef RG_STATIC_WORKSPACE_BYTES
 #define RG_STATIC_WORKSPACE_BYTES (64ull << 20)
+#endif
 
-/* rg_run without a caller workspace, for callers that cannot allocate
- * device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc). No counterpart in the reference: its
- * runtime always allocates scratch per call (runtime.py:538-542).
+/* rg_run without a caller workspace. No counterpart in the reference; for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).
  *
  * The workspace is a static device array of RG_STATIC_WORKSPACE_BYTES per
- * device, held from the first rg_module_create on that device until the
- * process ends. Plans whose workspace_bytes exceed it fail with
- * RG_E_WORKSPACE before anything is launched (rg_run takes any size). Every
- * call on a device shares that device's array, and each call initialises
- * every counter and table its kernels read, so no contents carry over;
- * calls that overlap on one device (two streams, or two host threads) race
- * on the array and must be serialised by the caller. Calls no allocating
- * routine: no hipMalloc, no event creation (rg_profile_* does not record
- * these calls). Same kernels and results as rg_run; a debug_visits module
- * is refused (it keeps its counters after a call). Enqueue only. */
+ * device: every process that loads the library holds it on each device it
+ * creates a module on, from the first rg_module_create there until the
+ * process ends, whether or not it calls this. Plans whose workspace_bytes
+ * exceed it fail with RG_E_WORKSPACE before anything is launched (rg_run
+ * takes any size). Every call on a device shares that device's array under
+ * rg_run's workspace contract, so results do not depend on earlier calls; a
+ * call that fails after launching part of its plan leaves the array marked,
+ * and the next call on that device first launches a one-workgroup kernel
+ * that returns its counters to zero. Calls that overlap on one device (two
+ * streams, or two host threads) race on the array and must be serialised by
+ * the caller. Calls no allocating routine: no hipMalloc, no event creation
+ * (rg_profile_* does not record these calls). Same kernels and results as
+ * rg_run; a debug_visits module is refused (it keeps its counters after a
+ * call). Enqueue only. */
 int rg_run_static(const rg_module* module, const rg_plan* plan, const void* values, const void* offsets,
                   void* out, const float* mask, void* stream);
+
+/* Test control: the next rg_run_static (any device) stops after `launches`
+ * kernel launches of its plan and fails with RG_E_DEVICE, as a launch error
+ * there would; -1 turns it off. No counterpart in the reference. */
+int rg_test_interrupt_static(int launches);
 
 /* Longest wait, in microseconds, of every softmax wait for statistics that
  * other workgroups publish, before the work is deferred: a register-resident
  * chunk's wait for the rest of its segment (default 2000; deferred chunks
- * are re-read by RG_ROLE_DEFERRED) and a streaming worker split part's wait
- * for its segment's statistics (default 1000000; deferred parts are
- * normalised by the worker's last workgroup). Results do not depend on it.
+ * are re-read once every item is handed out, by the same kernel), the
+ * re-read's own wait, and a streaming worker split part's wait for its
+ * segment's statistics (default 1000000; deferred parts are normalised by
+ * the worker's last workgroup; a fused softmax's re-read left undone by its
+ * wait is finished by that kernel's last workgroup). Results do not depend on it.
  * A test and diagnostics control: 0 makes every such wait that does not
  * succeed at once take the deferred path; -1 restores both defaults. */
 int rg_module_set_spin_limit(rg_module* module, int64_t microseconds);

@@ -116,6 +116,13 @@ constexpr int kMaxDevices = 64;
 constexpr size_t kScratchCounterBytes = (size_t)rg::kTicketStride * 8 * (1 + 2 * rg::kTicketLanes);
 std::mutex g_scratch_mutex;
 void* g_scratch[kMaxDevices];          // device address of `scratch` on each device, or null
+// A call on the device's static workspace failed after it had launched
+// something, so its counters may be set: the next call first launches
+// k_reset.
+bool g_scratch_dirty[kMaxDevices];
+// Test control (rg_test_interrupt_static): the next rg_run_static stops after
+// this many launches and fails, as a launch error would; -1: off.
+int g_interrupt_after = -1;
 
 }  // namespace
 
@@ -140,10 +147,16 @@ static int set_up_static_scratch(int device) {
   return RG_OK;
 }
 
-static void* static_scratch(int device) {
+static void* static_scratch(int device, bool* dirty) {
   if (device < 0 || device >= kMaxDevices) return nullptr;
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  *dirty = g_scratch_dirty[device];
   return g_scratch[device];
+}
+
+static void set_scratch_dirty(int device, bool dirty) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  g_scratch_dirty[device] = dirty;
 }
 
 // Event pool of a profiling session: launches+1 events per recorded call.
@@ -164,14 +177,22 @@ struct rg_module {
   const void* roles[RG_ROLE_COUNT];
   int64_t resident[RG_ROLE_COUNT];
   uint32_t lds[RG_ROLE_COUNT];
-  bool fused;                 // softmax through k_softmax_fused (+ k_softmax_deferred)
+  bool fused;                 // softmax through k_softmax_fused
   int64_t spin_ticks;         // wall-clock ticks of a chunk's bounded wait
-  int64_t drain_ticks;        // wall-clock ticks of a worker split part's wait for its statistics
+  int64_t drain_ticks;        // wall-clock ticks of a worker split part's (deferred chunk's) wait for its statistics
+  int64_t fold_ticks;         // wall-clock bound of a fold whose inputs are all published before it starts
   int64_t clock_khz;          // wall-clock rate
   int64_t* trace;             // item timeline buffer (diagnostics) or null
   int64_t trace_cap;
   mutable Profile profile;
 };
+
+// One past the last byte of the register-resident softmax's arena (the pair
+// table through the deferred list), 256-byte aligned.
+static uint64_t arena_end(const rg_plan* plan) {
+  const uint64_t end = plan->buffer_offset[RG_BUF_DEFERRED] + plan->buffer_bytes[RG_BUF_DEFERRED];
+  return (end + kAlign - 1) / kAlign * kAlign;
+}
 
 extern "C" {
 
@@ -286,19 +307,18 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
     delete module;
     return fail(RG_E_INVALID, "no compiled kernel for this dtype/feature geometry");
   }
-  // k_init runs only before the register-resident softmax (its pair slots);
-  // otherwise k_classify initialises what a call uses. Every classified
-  // call's last workgroup returns the counters to zero.
-  module->roles[RG_ROLE_INIT] = rg::kernel_init();
+  // k_classify initialises what a call uses; every classified call's last
+  // workgroup returns the counters to zero (RG_ROLE_INIT and
+  // RG_ROLE_DEFERRED stay empty: the register-resident softmax needs no
+  // slot fill and drains its deferred chunks and wave class itself).
   module->roles[RG_ROLE_CLASSIFY] = rg::kernel_classify(spec.offsets_dtype);
   module->roles[RG_ROLE_WORKER] = k.worker;
   // RG_ROLE_SPLIT_NORMALIZE stays empty: k_worker normalises split parts.
   module->roles[RG_ROLE_NAIVE] = k.naive;
   const bool f32_logits = spec.has_mask != 0 || spec.scale != 1.0f;
   const void* fused = f32_logits ? k.fused_f32 : k.fused;
-  module->fused = fused && k.deferred && rg_spec_uses_fused(&spec) == 1;
+  module->fused = fused && rg_spec_uses_fused(&spec) == 1;
   module->roles[RG_ROLE_FUSED] = module->fused ? fused : nullptr;
-  module->roles[RG_ROLE_DEFERRED] = module->fused ? k.deferred : nullptr;
 
   int previous = 0;
   err = hipGetDevice(&previous);
@@ -324,6 +344,10 @@ int rg_module_create(int device, const rg_spec* spec_in, rg_module** out) {
   // before it is left to the grid's last workgroup (the wait normally ends
   // in microseconds).
   module->drain_ticks = module->clock_khz * 1000;
+  // A fold whose every input was published before it started (a tree
+  // group's last arriver, the last workgroup's drain) normally succeeds at
+  // once; it polls for at most 1 s.
+  module->fold_ticks = module->clock_khz * 1000;
   for (int role = 0; role < RG_ROLE_COUNT && err == hipSuccess; ++role) {
     module->resident[role] = 0;
     module->lds[role] = 0;
@@ -477,11 +501,11 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     add_launch(RG_ROLE_NAIVE, b, tiles_block);
     return RG_OK;
   }
-  // Workgroups for grid-stride batches of at most B wave-class segments:
-  // the fewest segments a workgroup takes per batch is one per wave.
-  const int64_t wave_batch_min = geo.flat ? rg::kBlock : rg::kWavesPerBlock;
-  const int64_t stride_grid = (b + wave_batch_min - 1) / wave_batch_min;
   if (schedule == RG_SHORT_SEGMENTS) {
+    // Workgroups for grid-stride batches of at most B wave-class segments:
+    // the fewest segments a workgroup takes per batch is one per wave.
+    const int64_t wave_batch_min = geo.flat ? rg::kBlock : rg::kWavesPerBlock;
+    const int64_t stride_grid = (b + wave_batch_min - 1) / wave_batch_min;
     // Batches of segments in order, grid-stride: no counters, no workspace.
     add_launch(RG_ROLE_WORKER, std::min(module->resident[RG_ROLE_WORKER], stride_grid), 1);
     return RG_OK;
@@ -523,9 +547,15 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
     if (!mul_ok(b, (int64_t)sizeof(rg::Item), &sizes[RG_BUF_BLOCK_ITEMS]) ||
         !mul_ok(items_cap, (int64_t)sizeof(rg::Item), &sizes[RG_BUF_ITEMS]) ||
         !mul_ok(items_cap, 8, &sizes[RG_BUF_DEFERRED]) || !mul_ok(items_cap, 4, &sizes[RG_BUF_ARRIVE]) ||
-        !mul_ok(b_split, 4, &sizes[RG_BUF_SEG_ARRIVE]) || !mul_ok(item_bytes, 2, &sizes[RG_BUF_PAIRS]) ||
+        !mul_ok(item_bytes, 2, &sizes[RG_BUF_PAIRS]) ||
         !mul_ok(rg::tree_group_rows(items_cap), (int64_t)d * 8, &sizes[RG_BUF_FINAL_PAIRS]))
       return fail(RG_E_INVALID, "fused softmax workspace bytes overflow");
+    // The work ticket counter counts tickets in 32 bits (the high half
+    // counts deferred chunks): items, segments and the wave-class batches
+    // stay far below 2^32.
+    if (b + items_cap > ((int64_t)1 << 31))
+      return fail(RG_E_INVALID, "register-resident softmax: more than 2^31 segments and chunks in one call; run this "
+                                "input through the naive program");
     // A merge folds a segment's pairs through one buffer resource, whose
     // offsets are 32-bit: the whole pair table stays below 2 GiB.
     if (sizes[RG_BUF_PAIRS] > INT32_MAX)
@@ -534,25 +564,41 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
   }
   plan->fused = module->fused ? 1 : 0;
   if (spec.debug_visits && !mul_ok(b, 4, &sizes[RG_BUF_VISITS])) return fail(RG_E_INVALID, "visits bytes overflow");
+  // The counters at offset 0 of every plan, then the register-resident
+  // softmax's arena -- the slots that hold zero between its calls (pairs,
+  // group rows, arrival and reader counters, deferred list) -- at one offset
+  // for every plan, then the rest, each 256-byte aligned.
+  static const int kOrder[RG_WORKSPACE_BUFFERS] = {
+      RG_BUF_COUNTERS, RG_BUF_PAIRS, RG_BUF_FINAL_PAIRS, RG_BUF_ARRIVE, RG_BUF_DEFERRED, RG_BUF_QUEUE,
+      RG_BUF_ITEM_POS, RG_BUF_PART_BEGIN, RG_BUF_PARTIALS, RG_BUF_PARTIAL_SUMS, RG_BUF_STATS_MAX,
+      RG_BUF_STATS_SUM, RG_BUF_VISITS, RG_BUF_SEG_ARRIVE, RG_BUF_ITEMS, RG_BUF_BLOCK_ITEMS};
   int64_t end = 0;
-  for (int i = 0; i < RG_WORKSPACE_BUFFERS; ++i) {
+  for (int k = 0; k < RG_WORKSPACE_BUFFERS; ++k) {
+    const int i = kOrder[k];
     const int64_t offset = (end + (int64_t)kAlign - 1) / (int64_t)kAlign * (int64_t)kAlign;
     plan->buffer_offset[i] = (uint64_t)offset;
     plan->buffer_bytes[i] = (uint64_t)sizes[i];
     if (!add_ok(offset, sizes[i], &end)) return fail(RG_E_INVALID, "workspace bytes overflow signed i64");
   }
-  plan->workspace_bytes = (uint64_t)end;
+  plan->workspace_bytes = (uint64_t)((end + (int64_t)kAlign - 1) / (int64_t)kAlign * (int64_t)kAlign);
 
   const int classify_block = b >= rg::kClassifyLarge ? rg::kClassifyBlock : rg::kBlock;
-  add_launch(RG_ROLE_CLASSIFY, (b + classify_block - 1) / classify_block, 1, classify_block);
+  int64_t classify_grid = (b + classify_block - 1) / classify_block;
   if (module->fused) {
-    // Grid-stride fill of the slots the call's merges poll (sized for the
-    // most: every item's pair, 8 per thread); the block and split classes
-    // held in registers; then the deferred chunks and the wave class, in the
-    // streaming worker's batches.
-    add_launch(RG_ROLE_INIT, std::min<int64_t>(1024, std::max<int64_t>(1, items_cap * d / (rg::kBlock * 8))), 1);
-    add_launch(RG_ROLE_FUSED, std::min(module->resident[RG_ROLE_FUSED], b + items_cap), 1);
-    add_launch(RG_ROLE_DEFERRED, std::min(module->resident[RG_ROLE_DEFERRED], std::max(items_cap, stride_grid)), 1);
+    // k_classify also zeroes what the workspace's last call left nonzero in
+    // the register-resident softmax's arena (about a third of the arena in
+    // a call over long segments): workgroups for 64 KiB of it each, at most
+    // 1024, beyond the segments' own.
+    const int64_t arena = (int64_t)(arena_end(plan) - plan->buffer_offset[RG_BUF_PAIRS]);
+    classify_grid = std::max(classify_grid, std::min<int64_t>(1024, (arena + 65535) / 65536));
+  }
+  add_launch(RG_ROLE_CLASSIFY, classify_grid, 1, classify_block);
+  if (module->fused) {
+    // The block and split classes held in registers, then the wave class in
+    // the streaming worker's batches and the deferred chunks, in one
+    // persistent launch: one resident wave of workgroups (the waits assume
+    // the grid is co-resident), fewer when there is less work.
+    add_launch(RG_ROLE_FUSED, std::min(module->resident[RG_ROLE_FUSED], std::max<int64_t>(1, b + items_cap)), 1);
     return RG_OK;
   }
   // One persistent worker drains the wave, block and split queues (as many
@@ -570,7 +616,8 @@ int rg_plan_create(const rg_module* module, int64_t n, int64_t b, int schedule, 
 // allocation-free entry point passes false.
 static int enqueue(const char* entry, const rg_module* module, const rg_plan* plan, const void* values,
                    const void* offsets, void* out, const float* mask, void* workspace, uint64_t workspace_bytes,
-                   void* stream, bool profiled) {
+                   void* stream, bool profiled, int* launched = nullptr, int stop_after = -1) {
+  if (launched) *launched = 0;
   if (!module || !plan) return fail(RG_E_INVALID, "%s: null module or plan", entry);
   const rg_spec& spec = module->spec;
   if ((mask != nullptr) != (spec.has_mask != 0)) return fail(RG_E_INVALID, "mask presence must match the module");
@@ -629,6 +676,13 @@ static int enqueue(const char* entry, const rg_module* module, const rg_plan* pl
     // margin of 1/8 covers workgroups that are slow to become resident.
     p.wait_parts = std::max<int64_t>(1, module->resident[RG_ROLE_FUSED] * 7 / 8);
     p.spin_ticks = module->spin_ticks;
+    p.fold_ticks = module->fold_ticks;
+    if (plan->fused) {
+      // The arena: from the pair table to the end of the deferred list.
+      const uint64_t first = plan->buffer_offset[RG_BUF_PAIRS];
+      p.arena = static_cast<unsigned char*>(workspace) + first;
+      p.arena_bytes = (int64_t)(arena_end(plan) - first);
+    }
     p.trace = module->trace;
     p.trace_cap = module->trace_cap;
   }
@@ -658,12 +712,17 @@ static int enqueue(const char* entry, const rg_module* module, const rg_plan* pl
       err = hipErrorInvalidDeviceFunction;
       break;
     }
+    if (stop_after >= 0 && i >= stop_after) {
+      if (previous != module->device) (void)hipSetDevice(previous);
+      return fail(RG_E_DEVICE, "%s: interrupted after %d launches (test control)", entry, i);
+    }
     if (record) mark();
     p.tiles = (int32_t)plan->grid[i][1];
     void* args[] = {&p};
     if (err == hipSuccess)
       err = hipLaunchKernel(fn, dim3(plan->grid[i][0], plan->grid[i][1], plan->grid[i][2]), dim3(plan->block[i]),
                             args, 0, s);
+    if (err == hipSuccess && launched) ++*launched;
   }
   if (record) mark();
   if (previous != module->device) (void)hipSetDevice(previous);
@@ -689,10 +748,43 @@ int rg_run_static(const rg_module* module, const rg_plan* plan, const void* valu
                 "rg_run_static: the plan needs %llu bytes of workspace; the static workspace holds at most %llu "
                 "(use rg_run with a caller-allocated workspace)",
                 (unsigned long long)plan->workspace_bytes, (unsigned long long)kStaticScratchBytes);
-  void* base = static_scratch(module->device);
+  bool dirty = false;
+  void* base = static_scratch(module->device, &dirty);
   if (!base) return fail(RG_E_DEVICE, "rg_run_static: no static workspace address for device %d", module->device);
-  return enqueue("rg_run_static", module, plan, values, offsets, out, mask, plan->workspace_bytes ? base : nullptr,
-                 plan->workspace_bytes, stream, false);
+  if (dirty && plan->workspace_bytes) {
+    // An earlier call failed part way: its counters back to zero first.
+    int previous = 0;
+    hipError_t err = hipGetDevice(&previous);
+    if (err == hipSuccess && previous != module->device) err = hipSetDevice(module->device);
+    if (err != hipSuccess) return hip_fail(err, "hipSetDevice");
+    rg::Params p;
+    std::memset(&p, 0, sizeof p);
+    p.counters = static_cast<int64_t*>(base);
+    void* args[] = {&p};
+    err = hipLaunchKernel(rg::kernel_reset(), dim3(1), dim3(rg::kBlock), args, 0, static_cast<hipStream_t>(stream));
+    if (previous != module->device) (void)hipSetDevice(previous);
+    if (err != hipSuccess) return hip_fail(err, "rg_run_static: static workspace reset");
+    set_scratch_dirty(module->device, false);
+  }
+  int launched = 0;
+  int stop_after = -1;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    std::swap(stop_after, g_interrupt_after);
+  }
+  const int status = enqueue("rg_run_static", module, plan, values, offsets, out, mask,
+                             plan->workspace_bytes ? base : nullptr, plan->workspace_bytes, stream, false, &launched,
+                             stop_after);
+  if (status != RG_OK && launched > 0) set_scratch_dirty(module->device, true);
+  return status;
+}
+
+int rg_test_interrupt_static(int launches) {
+  if (launches < -1 || launches >= RG_MAX_LAUNCHES)
+    return fail(RG_E_INVALID, "rg_test_interrupt_static: launches must be -1 or in [0, %d)", RG_MAX_LAUNCHES);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  g_interrupt_after = launches;
+  return RG_OK;
 }
 
 int rg_check_offsets(int device, int offsets_dtype, const void* offsets, int64_t n, int64_t b, int64_t min_len,

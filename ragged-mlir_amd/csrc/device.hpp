@@ -58,9 +58,19 @@ constexpr int kDirect = 16;            // register-resident softmax: chunks merg
 constexpr int kTreeGroup = 16;         // register-resident softmax: chunks per first-level tree group
 constexpr int kGroupRowSlot = 10;      // counters slot: final_pairs rows reserved by tree-merged segments
 constexpr int kDoneSlot = 11;          // counters slot: workgroups of the call's last kernel finished
+// counters slot: the state of the register-resident softmax's arena (the
+// slots its merges poll, which must hold zero while unpublished): 0 = the
+// workspace is as allocated (all zero); 1 = not known to be zero (another
+// plan's buffers overlap it); v >= 2 = its first v - 2 bytes are zero but for
+// the kDirtyRanges byte ranges at slots kDirtySlot.. (the pairs and group
+// rows the last call published). The call's last workgroup sets them
+// (reset_counters); k_classify zeroes what a plan's arena needs.
+constexpr int kCleanSlot = 12;
+constexpr int kDrainSlot = 13;         // counters slot: deferred chunks claimed by the register-resident softmax's drain
+constexpr int kDirtySlot = 14;         // counters slots 14-19: [begin, end) byte ranges of the arena left nonzero
+constexpr int kDirtyRanges = 3;
 constexpr int kDirectDone = 64;        // up to this many active workgroups count out on kDoneSlot alone
 constexpr int32_t kStatsReady = -1;     // seg_arrive[k] once a split segment's softmax statistics are published
-constexpr uint32_t kSentinel = 0x7F800001u;  // unpublished (m, s) pair: signalling-NaN s bits
 
 // Rows of final_pairs (register-resident softmax): one per first-level group
 // of every segment merged by tree. Such a segment has more than kDirect of
@@ -119,18 +129,29 @@ struct ExpShift {
   }
 };
 
-// e = exp(x - m) in [0, 1] of bf16 rows held in registers between the two
-// passes of the register-resident softmax, as 16-bit unsigned normalised
-// integers (v_cvt_pknorm_u16_f32, round to nearest): an absolute error of at
-// most 2^-17, far below the bf16 output's own rounding, where storing e as
-// bf16 would round twice. NaN stores as 0; a NaN e only occurs in columns
-// whose scale factor is NaN, so the output stays NaN.
-constexpr float kUnormScale = 1.0f / 65535.0f;
-__device__ __forceinline__ uint32_t pack_unorm(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pknorm_u16(lo, hi));
-}
-__device__ __forceinline__ float unorm_lo(uint32_t w) { return (float)(w & 0xffffu); }
-__device__ __forceinline__ float unorm_hi(uint32_t w) { return (float)(w >> 16); }
+// The softmax output y = exp(x - M) / S of one column with statistics
+// (M, S), rounded once to T. bf16 outputs: y = 2^(x log2(e) - c) with
+// c = M log2(e) + log2(S), one FMA into v_exp_f32 per element (c is rounded
+// once per column; its error, below 2^-24 |c| in the exponent, is far below
+// a bf16 ulp), so no intermediate value can underflow before the output does.
+// f32 outputs: exp_split(x - M) * (1 / S), the reference's exp(x - m) / s
+// (ToGPU.cpp:712-733) with the division as a rounded reciprocal. Special
+// columns follow IEEE arithmetic: M = -inf (only -inf, S = 0), NaN M or S
+// give NaN everywhere; x = -inf in a finite column gives 0.
+template <class T>
+struct Normalizer {
+  float a = 0.f, b = 0.f;   // bf16: a = -c; f32: a = M, b = 1 / S
+  Normalizer() = default;
+  __device__ Normalizer(float a_, float b_) : a(a_), b(b_) {}
+  __device__ static Normalizer of(float m, float s) {
+    if constexpr (std::is_same<T, float>::value) return Normalizer(m, 1.0f / s);
+    else return Normalizer(-__builtin_fmaf(m, kLog2eHi, __builtin_amdgcn_logf(s)), 0.f);
+  }
+  __device__ float operator()(float x) const {
+    if constexpr (std::is_same<T, float>::value) return exp_split(x - a) * b;
+    else return __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2eHi, a));
+  }
+};
 
 // Workgroup-wide OR of `x` for the kBlock-thread workgroups of every kernel
 // here: one ballot per wave, one LDS flag per wave, two barriers. HIP's
@@ -178,16 +199,16 @@ struct Params {
   int64_t part_rows;       // rows per split part
   int64_t items_cap;       // capacity of the split item tables
   int64_t b_split;         // capacity of the split queue / statistics rows
-  int64_t* counters;       // slots 0-11: wave (reduced alone), block, split segment
+  int64_t* counters;       // slots 0-13: wave (reduced alone), block, split segment
                            //      counts; split items; work ticket; deferred
                            //      chunks (register-resident softmax) or split
                            //      parts (worker softmax); tree items; the wave
                            //      count of a register-resident softmax; the rest
                            //      of the wave class; the split-part normalisation
                            //      ticket; final_pairs rows reserved; done lanes
-                           //      finished. Then the
-                           //      worker's ticket lanes and the done lanes
-                           //      (kTicketStride apart)
+                           //      finished; the arena's clean extent; deferred
+                           //      chunks claimed. Then the worker's ticket lanes
+                           //      and the done lanes (kTicketStride apart)
   int64_t* queue;          // [3, B] original segment ids per class
   int64_t* item_pos;       // [items_cap] split-queue position of each item
   int64_t* part_begin;     // [B] first item of each split-queue position
@@ -196,17 +217,22 @@ struct Params {
   float* stats_max;        // [B_split, D] combined softmax reference
   float* stats_sum;        // [B_split, D] combined softmax mass
   int32_t* visits;         // [B] or null (debug)
-  int64_t* deferred;       // [items_cap] chunks left to the re-read pass (register-resident
-                           // softmax); [items_cap * tiles] split parts left to the last
-                           // workgroup (worker softmax)
-  int32_t* arrive;         // [items_cap] chunk arrivals per 32-chunk group (slot: group's first item)
-  int32_t* seg_arrive;     // [B_split] group arrivals per split segment
+  int64_t* deferred;       // [items_cap] 1 + item of each chunk left to the drain, 0 while unwritten
+                           // (register-resident softmax); [items_cap * tiles] split parts left
+                           // to the last workgroup (worker softmax)
+  int32_t* arrive;         // [items_cap] register-resident softmax: a tree group's chunk arrivals
+                           // (at the group's first item); a segment's readers of its merged
+                           // statistics (first item of a direct segment, second of a tree one)
+  int32_t* seg_arrive;     // [B_split] part arrivals per split segment (worker)
   Item* items;             // [items_cap] split chunks (register-resident softmax)
   Item* block_items;       // [B] whole segments (register-resident softmax)
   uint64_t* pairs;         // [items_cap, D] published (m, s) of each chunk
   uint64_t* final_pairs;   // [tree_group_rows(items_cap), D] (M, S) of each group of a tree-merged segment
   int64_t spin_ticks;      // wall-clock ticks a chunk waits for its segment before deferring
-  int64_t drain_ticks;     // wall-clock bound of a split part's wait for its segment's statistics
+  int64_t drain_ticks;     // wall-clock bound of a split part's (a deferred chunk's) wait for its segment's statistics
+  int64_t fold_ticks;      // wall-clock bound of a fold whose every input is published before it starts
+  unsigned char* arena;    // register-resident softmax: pairs, final_pairs, arrive and deferred, contiguous
+  int64_t arena_bytes;     // their bytes (a multiple of 256), 0 for every other plan
   int64_t wait_parts;      // longest segment (in chunks) whose chunks wait for each other
   int64_t* trace;          // [trace_cap, 8] item timeline or null (diagnostics)
   int64_t trace_cap;

@@ -3,14 +3,15 @@
 //
 // Items (descriptors written by k_classify): every chunk of every
 // split-class segment (ceil(L / part_rows) chunks, contiguous in the queue),
-// then every block-class segment (wave-class segments are batched by
-// k_softmax_deferred after this kernel). A 256-thread workgroup takes the next item
+// then every block-class segment. A 256-thread workgroup takes the next item
 // with one atomic ticket (and prefetches the following descriptor while it
-// finishes) and holds its rows in registers (RPT rows per thread):
+// finishes) and holds its rows in registers (RPT rows per thread), as loaded:
 //   1. m = column max of the rows (IEEE maximum: NaN propagates);
-//   2. e = exp(x - m) replaces x in registers, s = column sum of e;
-//   3. whole segment: y = e / s.  Chunk of a longer segment: publish (m, s),
-//      get the segment's merged (M, S) and write y = e * exp(m - M) / S.
+//   2. s = column sum of exp(x - m);
+//   3. whole segment: y = exp(x - m) / s from the held rows.  Chunk of a
+//      longer segment: publish (m, s), get the segment's merged (M, S) and
+//      write y = exp(x - M) / S from the held rows (Normalizer: every output
+//      one rounding of an f32 value).
 // Merging is deterministic (folds in chunk order). Up to kDirect chunks:
 // every chunk reads all published pairs itself. Longer: the last chunk of
 // each group of kGroup folds the group and publishes it, every chunk folds
@@ -21,10 +22,25 @@
 // by a running workgroup whenever the device holds all chunks of the
 // segment at once. Segments with more chunks than that (wait_parts), and
 // chunks whose spin limit passes, skip the wait: they drop their registers
-// and k_softmax_deferred re-reads them after this kernel. A wait for chunks
-// not yet handed out also ends when the ticket counter stalls (fewer
-// workgroups resident than the plan assumed: another process on the
-// device). No wait is unbounded.
+// and are re-read by the kernel's drain once every ticket is handed out. A
+// wait for chunks not yet handed out also ends when the ticket counter
+// stalls (fewer workgroups resident than the plan assumed: another process
+// on the device). No wait is unbounded.
+//
+// After the items, the same tickets hand out the wave class in the
+// streaming worker's batches (a ticket per short segment would serialise the
+// kernel on its counter), then the workgroups drain the deferred chunks; the
+// last workgroup out drains what is left and returns the counters to zero.
+// One launch after k_classify does the whole call.
+//
+// Every slot a merge polls (pairs, group rows, group arrival counters, the
+// deferred list: the arena) holds zero while unpublished, so a pair that is
+// not yet visible is never taken for a published one. A workspace is zero
+// when allocated; the call returns the counters and the deferred list to
+// zero itself, and its last workgroup records the byte ranges of the pairs
+// and group rows it published, which the next call's k_classify zeroes with
+// many workgroups before this kernel starts (zeroing them here, by each
+// segment's last reader, cost this kernel 3.5%).
 //
 // Reference semantics: docs/semantics.md (softmax row), the reference's
 // online statistics and merge algebra (ToGPU.cpp:486-557, 435-472) restated
@@ -44,6 +60,15 @@ constexpr int kGroup = kTreeGroup;   // chunks merged per first-level group
 // to 127 than at 2. Polling feature 0 of each slot between folds (128x
 // fewer bytes) was 8% slower: the extra round trip delays every wake-up.
 constexpr int kPollSleep = 64;
+
+// The work ticket counter (counters[4]) holds two counts: tickets handed out
+// (low 32 bits) and chunks deferred to the drain (high 32 bits; a deferral
+// adds 2^32 and takes its deferred-list slot from the old value). Every
+// ticket fetch so also tells a workgroup how many chunks were deferred by
+// then, and a workgroup that leaves having seen none -- the common case --
+// leaves without a further round trip. The plan keeps tickets below 2^32.
+constexpr uint64_t kTicketMask = 0xffffffffull;
+constexpr int kDeferShift = 32;
 
 // Buffer addressing: a wave-uniform 128-bit resource (base in SGPRs) per
 // chunk, covering exactly the chunk's bytes, and one per-thread byte offset
@@ -214,10 +239,11 @@ __device__ __forceinline__ void block_allreduce(float (&v)[VEC], int lpr, int fe
 // Statistics shared between workgroups travel only through agent-scope
 // atomic stores and loads (coherent across the XCDs' L2 caches), so no
 // L2-wide writeback or invalidate is needed. Each (m, s) pair of a feature is
-// one 64-bit store; k_init fills every slot (chunk pairs and group rows)
-// with a sentinel first (s bits 0x7F800001, a signalling NaN, which f32
-// arithmetic never produces), so a
-// reader polls the data itself instead of a separate flag. A publisher that
+// one 64-bit store into a slot that holds zero until then: a published pair
+// is never zero (a finite m comes with s >= 1, as the column's largest row
+// contributes exp(0); m = -inf and NaN have nonzero bits), so a reader polls
+// the data itself instead of a separate flag, and a pair that is not yet
+// visible reads as unpublished, never as a stale value. A publisher that
 // bumps a counter waits for its stores to complete (s_waitcnt vmcnt(0))
 // before the barrier after which one thread updates the counter.
 __device__ __forceinline__ uint64_t pack_pair(float m, float s) {
@@ -225,20 +251,16 @@ __device__ __forceinline__ uint64_t pack_pair(float m, float s) {
 }
 __device__ __forceinline__ float pair_m(uint64_t v) { return __uint_as_float((uint32_t)v); }
 __device__ __forceinline__ float pair_s(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
-__device__ __forceinline__ bool pair_ready(uint64_t v) { return (uint32_t)(v >> 32) != kSentinel; }
+__device__ __forceinline__ bool pair_ready(uint64_t v) { return v != 0; }
 __device__ __forceinline__ void store_pair(uint64_t* p, float m, float s) {
   __hip_atomic_store(p, pack_pair(m, s), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t load_pair(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Wait for this wave's outstanding vector memory operations (vmcnt = 0).
 __device__ __forceinline__ void wait_stores() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Segments of at most kDirect chunks merge directly: every chunk reads all
 // chunks' pairs. Longer ones fold groups of kGroup chunks (last arriver) and
-// then the groups (last group), and publish (M, S) in final_pairs; a
-// segment of one group publishes it from the group fold.
+// every chunk then folds the segment's group rows.
 constexpr int kBatch = 8;            // pair loads in flight per thread
 
 // Pair loads of a fold go through one wave-uniform resource over the slots
@@ -258,7 +280,7 @@ __device__ __forceinline__ uint64_t load_pair_at(Rsrc r, int voffset, int soffse
 
 // One thread's fold of `count` slots, slot_bytes apart, starting voff bytes
 // into resource r, in slot order, kBatch loads at a time; ok turns false if
-// a slot still holds the sentinel.
+// a slot is still unpublished.
 __device__ __forceinline__ State<OP_SOFTMAX> fold_range(Rsrc r, int voff, int count, int slot_bytes, bool& ok) {
   State<OP_SOFTMAX> acc;
   acc.init();
@@ -285,7 +307,7 @@ __device__ __forceinline__ State<OP_SOFTMAX> fold_range(Rsrc r, int voff, int co
 // R * d <= 256 and R <= count) fold R contiguous ranges of slots at once;
 // the R range results are folded in range order through `stage` (R * d
 // pairs). The association depends only on (count, d): deterministic. True,
-// after a barrier, when no slot held the sentinel.
+// after a barrier, when every slot was published.
 // The thread index through an opaque copy: values derived from it inside a
 // persistent kernel's loop are recomputed where they are used (a few
 // integer instructions) instead of being hoisted before the loop and kept
@@ -337,6 +359,20 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
   return all;
 }
 
+// fold_block until every slot is published or `ticks` of wall clock pass
+// (thread 0 decides, so the workgroup agrees); false when it gave up.
+__device__ __forceinline__ bool poll_fold(const uint64_t* base, int64_t count, int d, int64_t ticks, float* lds_m,
+                                          float* lds_s, uint64_t* stage) {
+  const long long start = wall_clock64();
+  for (;;) {
+    if (fold_block(base, count, 1, d, lds_m, lds_s, stage)) return true;
+    bool give_up = false;
+    if (threadIdx.x == 0) give_up = wall_clock64() - start >= ticks;
+    if (block_any(give_up)) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
 // A wait also ends, before its budget, once the segment still has chunks
 // not handed out (ticket counter <= last_ticket) and the ticket counter has
 // not moved over an interval of spin_ticks / kStallDivisor (100 us with the
@@ -367,8 +403,8 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
       const long long now = wall_clock64();
       give_up = now - start >= spin_ticks;
       if (!give_up && now >= next_check) {
-        const int64_t handed = __hip_atomic_load(const_cast<int64_t*>(tickets), __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t handed = (int64_t)((uint64_t)__hip_atomic_load(const_cast<int64_t*>(tickets), __ATOMIC_RELAXED,
+                                                                     __HIP_MEMORY_SCOPE_AGENT) & kTicketMask);
         give_up = handed == seen && handed <= last_ticket;
         seen = handed;
         next_check = now + interval;
@@ -379,14 +415,45 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
   }
 }
 
+// A value the compiler cannot see through, made where it is used: constants
+// of rarely taken branches inside the persistent loop are then not hoisted
+// out of it and held in registers (or spilled) while the rows are live.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// A chunk's segment: its first item and its merged statistics (the chunks'
+// pairs of a direct segment, the group rows of a tree one).
+struct SegmentStats {
+  const uint64_t* base;   // first slot of the statistics a reader folds
+  int64_t count;          // slots (chunks or groups) they span, d pairs each
+};
+__device__ __forceinline__ SegmentStats segment_stats(const Params& p, int64_t idx, int32_t c, int32_t parts,
+                                                      int32_t k) {
+  SegmentStats st;
+  if (parts <= kDirect) {
+    st.base = p.pairs + (idx - c) * p.d;
+    st.count = parts;
+  } else {
+    st.base = p.final_pairs + (int64_t)k * p.d;
+    st.count = (parts + kGroup - 1) / kGroup;
+  }
+  return st;
+}
+
 // Counter-based first level of a long segment's merge: the last chunk of
 // each group of kGroup folds the group and publishes it in the segment's
-// row gbase + group of final_pairs (sentinel-filled, like every pair slot).
-// The fold never waits: every slot it reads was published (stores complete,
-// then the barrier) before the counter increment that made this workgroup
-// the last. The segment's chunks then fold its groups' rows directly, as a
-// directly merged segment folds its chunks' pairs: no second counter level,
-// whose store, atomic, fold and store again would sit on every chunk's wait.
+// row gbase + group of final_pairs. Every chunk of the group stored its pair
+// (agent scope), waited for the stores to complete and only then counted
+// itself, so the fold normally succeeds at once; a pair not yet visible
+// reads as zero and the fold polls again (a fold that never completes
+// within fold_ticks publishes NaN: the segment's output is then NaN, never
+// silently wrong). It returns the group's counter to zero (every chunk of
+// the group has counted). The segment's chunks then
+// fold its groups' rows directly, as a directly merged segment folds its
+// chunks' pairs: no second counter level, whose store, atomic, fold and
+// store again would sit on every chunk's wait.
 __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t gbase, int* flag_s,
                            float* lds_m, float* lds_s, uint64_t* stage) {
   const int t = local_tid();
@@ -402,9 +469,17 @@ __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t
   const bool last_in_group = *flag_s != 0;
   __syncthreads();
   if (!last_in_group) return;
-  (void)fold_block(p.pairs + gfirst * d, gsize, 1, d, lds_m, lds_s, stage);
-  for (int f = t; f < d; f += kBlock) store_pair(p.final_pairs + (gbase + group) * d + f, lds_m[f], lds_s[f]);
+  const bool ok = poll_fold(p.pairs + gfirst * d, gsize, d, p.fold_ticks, lds_m, lds_s, stage);
+  for (int f = t; f < d; f += kBlock) {
+    const float nan = __uint_as_float(opaque_u32(0x7fc00000u));
+    store_pair(p.final_pairs + (gbase + group) * d + f, ok ? lds_m[f] : nan, ok ? lds_s[f] : nan);
+  }
+  if (t == 0) p.arrive[gfirst] = 0;
 }
+
+template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
+__device__ void drain_and_finish(const Params& p, int64_t active, bool seen, float* lds_m, float* lds_s,
+                                 uint64_t* stage, int* flag_s, int64_t* claim_s);
 
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) void k_softmax_fused(Params p) {
@@ -413,13 +488,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   using Store = typename std::conditional<STORE_F32, float, T>::type;
   using In = Words<T, VEC>;
   using Reg = Words<Store, VEC>;
-  // Pass 1 replaces each row by e = exp(x - m) and pass 2 writes e times the
-  // column's factor exp(m - M) / S. f32 rows (f32 data, or the f32 logits a
-  // scale or mask makes of bf16 data) keep e in f32; bf16 rows keep it as a
-  // 16-bit unorm (pack_unorm), whose 1/65535 the factor carries, so the
-  // output is rounded to bf16 once.
-  constexpr bool kUnorm = !STORE_F32 && !std::is_same<T, float>::value;
-  // lds: reductions, then the segment's merged max per feature; lds_s: its sum.
+  // lds: reductions, then the segment's merged max per feature, then the
+  // normaliser's first constant; lds_s: the merged sum, then its second.
   __shared__ float lds[kBlock * VEC];
   __shared__ float lds_s[kBlock * VEC];
   __shared__ uint64_t stage[kBlock];    // partial folds of the segment merge
@@ -444,11 +514,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   const int wave_row0 = wave_rows ? __builtin_amdgcn_readfirstlane((t / kWave) * RPT * rstep) : 0;
   // Ticket order: chunks of segments merged by tree (top of the item
   // array), chunks of segments merged directly (bottom), block-class
-  // segments, wave-class segments (far end of block_items). k_classify
-  // counts a register-resident program's wave class in counters[7] instead
-  // of counters[0] -- k_softmax_deferred takes it after this kernel -- so
-  // the last term is 0. It stays: without it the compiler allocates this
-  // kernel's scalar registers differently and it runs slower.
+  // segments; then the wave class (after this loop). k_classify counts a
+  // register-resident program's wave class in counters[7] instead of
+  // counters[0], so the last term is 0. It stays: without it the compiler
+  // allocates this kernel's scalar registers differently and it runs slower.
   // The class counts were written by k_classify and stay fixed during this
   // kernel: read through the constant address space they load into SGPRs
   // (scalar loads) instead of occupying vector registers, which the held
@@ -457,7 +526,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   const int64_t n_tree = counts[6] < p.items_cap ? counts[6] : p.items_cap;
   const int64_t n_direct = counts[3] < p.items_cap - n_tree ? counts[3] : p.items_cap - n_tree;
   const int64_t n_split = n_tree + n_direct;
-  const int64_t n_block = counts[1];
+  const int64_t n_block = counts[1] < p.b ? counts[1] : p.b;
   const int64_t total = n_split + n_block + counts[0];
   const int64_t d = p.d;
   // Byte offsets inside an item: per thread, and the stride between a
@@ -479,7 +548,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   };
   if (t == 0) next_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
   __syncthreads();
-  int64_t ticket = uniform64(next_s);
+  int64_t ticket = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
   Item it;
   if (ticket < total) it = item_at(ticket);
   while (ticket < total) {
@@ -573,11 +642,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     int64_t next = 0;
     Item next_it;
     if (opaque(early)) {
-      next = uniform64(next_s);
+      next = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
       if (next < total) next_it = item_at(next);
     }
-    // 2. e = exp(x - m) in place, column sums. A column of only -inf has no
-    //    mass: its reference is taken as 0 so that e = 0, not NaN.
+    // 2. Column sums of exp(x - m); the rows stay as loaded. A column of
+    //    only -inf has no mass: its reference is taken as 0 so that every
+    //    term is 0, not NaN.
     float sum[VEC];
     ExpShift<T> ex[VEC];
 #pragma unroll
@@ -588,24 +658,11 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
       if (!live(i)) continue;
-      float e[VEC];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        e[v] = ex[v](Reg::get(data[i], v));
-        sum[v] += e[v];
-      }
-      if constexpr (kUnorm) {
-        if constexpr (VEC == 1) {
-          data[i][0] = pack_unorm(e[0], 0.f) & 0xffffu;
-        } else {
+      for (int v = 0; v < VEC; ++v) sum[v] += ex[v](Reg::get(data[i], v));
+    }
 #pragma unroll
-          for (int w = 0; w < Reg::kCount; ++w) data[i][w] = pack_unorm(e[2 * w], e[2 * w + 1]);
-        }
-      } else {
-        Reg::set(data[i], e);
-      }
-      // Pack now, so that the f32 values die here rather than after the
-      // reduction below.
+    for (int i = 0; i < RPT; ++i) {
 #pragma unroll
       for (int w = 0; w < Reg::kCount; ++w) asm volatile("" : "+v"(data[i][w]));
     }
@@ -621,12 +678,15 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       }
     }
     __syncthreads();
-    // 3. Scale factor per column, into lds[f]: exp(m - M) / S (times
-    //    1/65535 for unorm rows).
-    const float unit = kUnorm ? kUnormScale : 1.0f;
+    // 3. The segment's statistics (M, S) per column -- the item's own for a
+    //    whole segment -- as the normaliser's constants into lds / lds_s.
     bool defer = false;
     if (!chunk) {
-      for (int f = t; f < d; f += kBlock) lds[f] = exp_out<T>(own_m[f] - own_m[f]) / own_s[f] * unit;
+      for (int f = t; f < d; f += kBlock) {
+        const Normalizer<T> n = Normalizer<T>::of(own_m[f], own_s[f]);
+        lds[f] = n.a;
+        lds_s[f] = n.b;
+      }
     } else {
       const int64_t idx = index_of(ticket);
       const int64_t first = idx - it.c;
@@ -646,36 +706,39 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
         defer = !ready;
         // Same thread wrote lds[f] / lds_s[f] in the fold: no barrier needed.
         if (ready) {
-          for (int f = t; f < d; f += kBlock) lds[f] = exp_out<T>(own_m[f] - lds[f]) / lds_s[f] * unit;
+          for (int f = t; f < d; f += kBlock) {
+            const Normalizer<T> n = Normalizer<T>::of(lds[f], lds_s[f]);
+            lds[f] = n.a;
+            lds_s[f] = n.b;
+          }
         }
       }
       if (t == 0 && defer) {
-        const int64_t slot = (int64_t)atomicAdd((unsigned long long*)(p.counters + 5), 1ull);
-        if (slot < p.items_cap) p.deferred[slot] = idx;
+        const int64_t slot = (int64_t)(atomicAdd((unsigned long long*)(p.counters + 4), 1ull << kDeferShift) >>
+                                       kDeferShift);
+        if (slot < p.items_cap)
+          __hip_atomic_store(p.deferred + slot, idx + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
     __syncthreads();
     if (t == 0 && !opaque(early)) taken = atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
     if (t == 0) stamp_s[3] = wall_clock64();
     if (!defer) {
-      // 4. Normalise from registers; rows past the item are dropped by the
-      //    resource's range check.
+      // 4. y = exp(x - M) / S from the held rows; rows past the item are
+      //    dropped by the resource's range check.
       const Rsrc out = make_rsrc(static_cast<T*>(p.out) + start * d, chunk_elems * (int64_t)sizeof(T));
       asm volatile("" : "+v"(voff));
-      float factor[VEC];
+      Normalizer<T> norm[VEC];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) factor[v] = g.active ? lds[g.feature + v] : 0.f;
+      for (int v = 0; v < VEC; ++v) norm[v] = g.active ? Normalizer<T>(lds[g.feature + v], lds_s[g.feature + v])
+                                                       : Normalizer<T>();
       __builtin_amdgcn_s_setprio(3);
 #pragma unroll
       for (int i = 0; i < RPT; ++i) {
         if (!live(i)) continue;
         float y[VEC];
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) {
-          const float e = kUnorm ? ((v & 1) ? unorm_hi(data[i][v >> 1]) : unorm_lo(data[i][v >> 1]))
-                                 : Reg::get(data[i], v);
-          y[v] = e * factor[v];
-        }
+        for (int v = 0; v < VEC; ++v) y[v] = norm[v](Reg::get(data[i], v));
         uint32_t w[In::kCount];
         In::set(w, y);
         buffer_store<In::kBytes>(out, voff + i * step_in, 0, w);
@@ -686,7 +749,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     if (!opaque(early)) {
       if (t == 0) next_s = (int64_t)taken;
       __syncthreads();
-      next = uniform64(next_s);
+      next = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
       if (next < total) next_it = item_at(next);
     }
     if (opaque(p.trace && ticket < p.trace_cap) && t == 0) {
@@ -703,91 +766,158 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     ticket = next;
     it = next_it;
   }
+  // The wave class, in the streaming worker's batches: the rest of the wave
+  // class one segment per wave (counters[8]), then the segments one lane
+  // group reduces alone (counters[7]). Their tickets follow the items'; this
+  // workgroup holds its first.
+  {
+    const int64_t n_coop = counts[8] < p.b ? counts[8] : p.b;
+    const int64_t n_wave = counts[7] < p.b ? counts[7] : p.b;
+    const int64_t batch = wave_batch_size<false, VEC>(p.d);
+    const int64_t n_coop_batches = (n_coop + kWavesPerBlock - 1) / kWavesPerBlock;
+    const int64_t tail = total + n_coop_batches + (n_wave + batch - 1) / batch;
+    while (ticket < tail) {
+      const int64_t i = ticket - total;
+      if (i < n_coop_batches) coop_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_coop);
+      else wave_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i - n_coop_batches, n_wave, false);
+      __syncthreads();
+      if (t == 0) next_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+      __syncthreads();
+      ticket = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
+    }
+  }
+  // The last ticket fetch (next_s, as fetched) counted the chunks deferred
+  // by then.
+  __shared__ int64_t claim_s;
+  const bool seen = ((uint64_t)uniform64(next_s) >> kDeferShift) != 0;
+  drain_and_finish<T, OffT, VEC, RPT, MASK, STORE_F32>(p, gridDim.x, seen, lds, lds_s, stage, &flag_s, &claim_s);
 }
 
-// Rows [r0, r1) of a deferred chunk with the arithmetic k_softmax_fused
-// would have used in registers, so a chunk's bits do not depend on whether
-// it waited: e = exp(x - ref) with the chunk's own reference, as a 16-bit
-// unorm for bf16 rows held as loaded (`unorm`), times the chunk's factor.
+// A deferred chunk (item idx): fold its segment's statistics (bounded by
+// `ticks`), then re-read its rows and write y = exp(x - M) / S with the
+// register path's arithmetic (the same Normalizer from the same fold), so
+// its bits do not depend on whether it waited. When the statistics do not
+// appear in time it returns false having written nothing -- unless `must` (the last
+// workgroup, after every other has finished: nothing can publish later),
+// which then writes NaN, so that a lost publication is never silent.
 template <class T, int VEC, bool MASK>
-__device__ __forceinline__ void renormalize_rows(const Params& p, const RowGeo& g, int64_t r0, int64_t r1, bool unorm,
-                                                 const float (&ref)[VEC], const float (&factor)[VEC]) {
-  if (!g.active) return;
-  T* out = static_cast<T*>(p.out);
-  for (int64_t r = r0 + g.row_lane; r < r1; r += g.rows_step) {
-    float x[VEC];
-    load_input<T, VEC, MASK>(p, r * p.d + g.feature, x);
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) {
-      float e = ExpShift<T>(ref[v])(x[v]);
-      if (unorm) e = unorm_lo(pack_unorm(e, 0.f));
-      x[v] = e * factor[v];
-    }
-    Elem<T>::template store<VEC>(out + r * p.d + g.feature, x);
+__device__ bool finish_deferred(const Params& p, int64_t idx, int64_t ticks, bool must, float* lds_m, float* lds_s,
+                                uint64_t* stage) {
+  const int t = threadIdx.x;
+  const Item it = p.items[idx];
+  const SegmentStats st = segment_stats(p, idx, it.c, it.parts, it.k);
+  const bool ok = poll_fold(st.base, st.count, p.d, ticks, lds_m, lds_s, stage);
+  if (!ok && !must) return false;
+  for (int f = t; f < p.d; f += kBlock) {
+    const float nan = __builtin_nanf("");
+    const Normalizer<T> n = ok ? Normalizer<T>::of(lds_m[f], lds_s[f]) : Normalizer<T>(nan, nan);
+    lds_m[f] = n.a;
+    lds_s[f] = n.b;
   }
+  __syncthreads();
+  const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
+  if (g.active) {
+    Normalizer<T> norm[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) norm[v] = Normalizer<T>(lds_m[g.feature + v], lds_s[g.feature + v]);
+    T* out = static_cast<T*>(p.out);
+    for (int64_t r = it.start + g.row_lane; r < it.start + it.rows; r += g.rows_step) {
+      float x[VEC];
+      load_input<T, VEC, MASK>(p, r * p.d + g.feature, x);
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) x[v] = norm[v](x[v]);
+      Elem<T>::template store<VEC>(out + r * p.d + g.feature, x);
+    }
+  }
+  if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
+  __syncthreads();
+  return true;
 }
 
-// Chunks that did not normalise in k_softmax_fused (spin limit, or a segment
-// longer than the device holds at once): re-read and normalise with the
-// segment's merged statistics, complete once k_softmax_fused has finished,
-// and the chunk's own column max, by the register path's arithmetic
-// (renormalize_rows). Then the wave class, which k_softmax_fused
-// does not take (k_classify counts it in counters[7]), in the streaming
-// worker's batches: a ticket per short segment would serialise
-// k_softmax_fused on its ticket counter.
-template <class T, class OffT, int VEC, bool MASK>
-__global__ __launch_bounds__(kBlock) void k_softmax_deferred(Params p) {
-  const int64_t count = p.counters[5] < p.items_cap ? p.counters[5] : p.items_cap;
-  const int64_t n_coop = p.counters[8];
-  const int64_t n_wave = p.counters[7];
-  const int64_t batch = wave_batch_size<false, VEC>(p.d);
-  // Grid-stride over each list: workgroups past the longest list have no
-  // work and leave now, touching no counter (active_workgroups).
-  const int64_t work = max(count, max((n_coop + kWavesPerBlock - 1) / kWavesPerBlock, (n_wave + batch - 1) / batch));
-  const int64_t active = active_workgroups(work);
-  if (blockIdx.x >= active) return;
+// Deferred chunks, once this workgroup's tickets have run out (every item is
+// then handed out, and every holder publishes its pair before it waits, so
+// every deferred chunk's statistics appear). A workgroup whose last ticket
+// fetch counted deferred chunks (`seen`) claims entries of the deferred list
+// in order while any is listed and finishes each (an entry whose statistics
+// do not appear within drain_ticks is left for the last workgroup); it then
+// counts out once its stores are complete. A workgroup that saw none counts
+// out at once: deferrals after its fetch are left to the others. The last
+// workgroup out finishes every entry still listed (all pairs are published
+// by then), returns the list and the counters to zero and records what the
+// call left nonzero in the arena.
+template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
+__device__ void drain_and_finish(const Params& p, int64_t active, bool seen, float* lds_m, float* lds_s,
+                                 uint64_t* stage, int* flag_s, int64_t* claim_s) {
   const int t = threadIdx.x;
-  const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
-  // The register-resident kernel that ran held bf16 rows as loaded (e as
-  // unorm) unless a scale or mask made f32 logits of them (its STORE_F32
-  // variant, e in f32).
-  const bool unorm = !MASK && !std::is_same<T, float>::value && !p.has_scale;
-  const float unit = unorm ? kUnormScale : 1.0f;
-  __shared__ float lds_m[kBlock * VEC], lds_s[kBlock * VEC];
-  __shared__ uint64_t stage[kBlock];
-  for (int64_t i = blockIdx.x; i < count; i += gridDim.x) {
-    const int64_t slot = p.deferred[i];
-    const Item it = p.items[slot];
-    // The chunk's own column max, from its rows: IEEE maximum is exact in
-    // any order, so it equals the register path's.
-    State<OP_MAX> own[VEC];
-    init_all<OP_MAX, VEC>(own);
-    fold_rows<OP_MAX, T, VEC, MASK>(p, g, it.start, it.start + it.rows, own);
-    block_reduce<OP_MAX, VEC>(own, g.lpr, g.feat_lane, lds_m);
-    // Every pair is published once k_softmax_fused has finished.
-    if (it.parts <= kDirect) (void)fold_block(p.pairs + (slot - it.c) * p.d, it.parts, 1, p.d, lds_m, lds_s, stage);
-    else (void)fold_block(p.final_pairs + it.k * p.d, (it.parts + kGroup - 1) / kGroup, 1, p.d, lds_m, lds_s, stage);
+  unsigned long long* claimed = (unsigned long long*)(p.counters + kDrainSlot);
+  unsigned long long* word = (unsigned long long*)(p.counters + 4);
+  const unsigned long long cap = (unsigned long long)p.items_cap;
+  auto listed = [&]() {
+    const unsigned long long n = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >> kDeferShift;
+    return n < cap ? n : cap;
+  };
+  while (seen) {
     __syncthreads();
-    if (g.active) {
-      float ref[VEC], factor[VEC];
-#pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        const int f = g.feature + v;
-        ref[v] = own[v].m == neg_inf() ? 0.f : own[v].m;
-        factor[v] = exp_out<T>(own[v].m - lds_m[f]) / lds_s[f] * unit;
+    if (t == 0) {
+      int64_t mine = -1;
+      unsigned long long c = __hip_atomic_load(claimed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (;;) {
+        if (c >= listed()) break;
+        if (__hip_atomic_compare_exchange_strong(claimed, &c, c + 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+          mine = (int64_t)c;
+          break;
+        }
       }
-      renormalize_rows<T, VEC, MASK>(p, g, it.start, it.start + it.rows, unorm, ref, factor);
+      // The entry's writer reserved it before storing it: wait for the store.
+      int64_t entry = 0;
+      if (mine >= 0) {
+        const long long t0 = wall_clock64();
+        while ((entry = __hip_atomic_load(p.deferred + mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == 0 &&
+               wall_clock64() - t0 < p.fold_ticks)
+          __builtin_amdgcn_s_sleep(2);
+      }
+      *claim_s = mine < 0 ? -1 : (entry > 0 ? ((mine << 32) | (entry - 1)) : -2);
     }
-    if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
     __syncthreads();
+    const int64_t claim = *claim_s;
+    if (claim == -1) break;
+    if (claim == -2) continue;    // never written in time: the last workgroup sees it
+    const int64_t slot = claim >> 32, idx = claim & 0xffffffffll;
+    if (finish_deferred<T, VEC, MASK>(p, idx, p.drain_ticks, false, lds_m, lds_s, stage) && t == 0)
+      __hip_atomic_store(p.deferred + slot, (int64_t)-1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  for (int64_t i = blockIdx.x; i * kWavesPerBlock < n_coop; i += gridDim.x)
-    coop_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_coop);
-  for (int64_t i = blockIdx.x; i * batch < n_wave; i += gridDim.x)
-    wave_batch<OP_SOFTMAX, T, OffT, VEC, false, MASK>(p, i, n_wave, false);
-  // The call's last kernel: its last workgroup returns the counters to zero.
-  __shared__ int flag_s;
-  if (last_out(p, &flag_s, active, false)) reset_counters(p);
+  // A workgroup that deferred or finished a chunk took part in the drain
+  // (its own deferral precedes its last fetch): its list stores must be
+  // visible to the last workgroup before it counts out.
+  if (!last_out(p, flag_s, active, seen)) return;
+  const int64_t listed_n = (int64_t)listed();
+  for (int64_t j = 0; j < listed_n; ++j) {
+    const int64_t entry = __hip_atomic_load(p.deferred + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (entry > 0) (void)finish_deferred<T, VEC, MASK>(p, entry - 1, p.fold_ticks, true, lds_m, lds_s, stage);
+  }
+  for (int64_t j = t; j < listed_n; j += kBlock) p.deferred[j] = 0;
+  // What this call left nonzero in the arena, for the next call's
+  // k_classify: the pairs of the direct chunks (bottom of the pair table)
+  // and of the tree chunks (top), and the group rows.
+  int64_t dirty[2 * kDirtyRanges];
+  {
+    const int64_t n_tree = p.counters[6] < p.items_cap ? p.counters[6] : p.items_cap;
+    const int64_t n_direct = p.counters[3] < p.items_cap - n_tree ? p.counters[3] : p.items_cap - n_tree;
+    const int64_t rows_cap = tree_group_rows(p.items_cap);
+    const int64_t rows = p.counters[kGroupRowSlot] < rows_cap ? p.counters[kGroupRowSlot] : rows_cap;
+    const int64_t pairs = p.pairs ? (const unsigned char*)p.pairs - p.arena : 0;
+    const int64_t finals = p.final_pairs ? (const unsigned char*)p.final_pairs - p.arena : 0;
+    const int64_t slot = (int64_t)p.d * 8;
+    dirty[0] = pairs;
+    dirty[1] = pairs + n_direct * slot;
+    dirty[2] = pairs + (p.items_cap - n_tree) * slot;
+    dirty[3] = pairs + p.items_cap * slot;
+    dirty[4] = finals;
+    dirty[5] = finals + rows * slot;
+  }
+  __syncthreads();
+  reset_counters(p, dirty);
 }
 
 }  // namespace rg

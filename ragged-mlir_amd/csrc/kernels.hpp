@@ -8,8 +8,7 @@
 //    901-998, with wave64 thresholds) and initialises the per-segment state
 //    the call uses; one persistent worker (worker.hpp) drains the queues
 //    (ToGPU.cpp:999-1045), and the call's last workgroup returns the
-//    counters to zero for the next call (last_out, reset_counters). The
-//    register-resident softmax also runs k_init first (its pair slots). A
+//    counters to zero for the next call (last_out, reset_counters). A
 //    split segment is cut into ceil(L / part_rows) parts -- proportional to
 //    its length instead of the reference's fixed 8 -- each processed by one
 //    workgroup; the last part folds them (ToGPU.cpp:399-472) and, for
@@ -448,44 +447,36 @@ __device__ __forceinline__ bool last_out(const Params& p, int* flag_s, int64_t a
 
 // Every counter of the workspace back to zero, so the next call's
 // k_classify starts from zero (the workspace's contract: all-zero before its
-// first call, left so by every call). A debug specialisation (visits set)
-// keeps its counters for inspection instead; its workspace is fresh per call.
-__device__ __forceinline__ void reset_counters(const Params& p) {
+// first call, left so by every call), and the arena's state recorded: a
+// register-resident softmax call leaves its arena zero but for `dirty` (the
+// byte ranges of the pairs and group rows it published, which the next
+// call's k_classify zeroes); any other call's buffers overlap that region,
+// so it records the arena as unknown (1). A debug specialisation (visits
+// set) keeps its counters for inspection instead; its workspace is fresh
+// per call.
+__device__ __forceinline__ void reset_counters(const Params& p, const int64_t* dirty = nullptr) {
   if (p.visits) return;
   const int t = threadIdx.x;
-  if (t < kTicketStride) p.counters[t] = 0;
+  if (t < kTicketStride) {
+    int64_t v = 0;
+    if (t == kCleanSlot) v = dirty ? p.arena_bytes + 2 : 1;
+    else if (dirty && t >= kDirtySlot && t < kDirtySlot + 2 * kDirtyRanges) v = dirty[t - kDirtySlot];
+    p.counters[t] = v;
+  }
   if (t < 2 * kTicketLanes) p.counters[kTicketStride * (1 + t)] = 0;
 }
 
 #ifdef RG_PROLOGUE_KERNELS
 // Defined in exactly one translation unit (kernels_common.hip).
 
-// Register-resident softmax, after k_classify: fill the statistics slots
-// this call's merges poll with the unpublished sentinel -- the pairs of the
-// directly merged chunks (the bottom counters[3] items) and the group rows
-// of the tree-merged segments (counters[kGroupRowSlot]) -- and zero the tree
-// chunks' group arrival counters (the top counters[6] items). A tree chunk's
-// own pair is read only after its group's counter says it is published, so
-// it needs no sentinel. Everything else a call uses k_classify initialises,
-// or the previous call's last workgroup returned to zero (the counters).
-// Grid-stride, 16-byte stores where the span allows.
-__global__ __launch_bounds__(kBlock) void k_init(Params p) {
-  const int64_t tid = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  const int64_t threads = (int64_t)gridDim.x * kBlock;
-  const int64_t n_tree = p.counters[6] < p.items_cap ? p.counters[6] : p.items_cap;
-  const int64_t n_direct = p.counters[3] < p.items_cap - n_tree ? p.counters[3] : p.items_cap - n_tree;
-  const int64_t rows_cap = tree_group_rows(p.items_cap);
-  const int64_t rows = p.counters[kGroupRowSlot] < rows_cap ? p.counters[kGroupRowSlot] : rows_cap;
-  const uint64_t sentinel = (uint64_t)kSentinel << 32;
-  const ulonglong2 two = {sentinel, sentinel};
-  auto fill = [&](uint64_t* slots, int64_t count) {   // slots: 256-byte aligned
-    ulonglong2* pairs2 = reinterpret_cast<ulonglong2*>(slots);
-    for (int64_t i = tid; i < count / 2; i += threads) pairs2[i] = two;
-    if (tid == 0 && (count & 1)) slots[count - 1] = sentinel;
-  };
-  fill(p.pairs, n_direct * p.d);
-  fill(p.final_pairs, rows * p.d);
-  for (int64_t i = p.items_cap - n_tree + tid; i < p.items_cap; i += threads) p.arrive[i] = 0;
+// A workspace's counters back to their between-calls state (zero, the
+// arena's clean extent none) after a call that failed part way may have left
+// them set: the allocation-free entry point launches it on its static
+// workspace before the next call on that device. One workgroup.
+__global__ __launch_bounds__(kBlock) void k_reset(Params p) {
+  const int t = threadIdx.x;
+  if (t < kTicketStride) p.counters[t] = t == kCleanSlot ? 1 : 0;
+  if (t < 2 * kTicketLanes) p.counters[kTicketStride * (1 + t)] = 0;
 }
 
 // Bin segments: wave (L <= t_wave), block (L <= t_block), split (longer).
@@ -509,6 +500,49 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
   // (back of the wave queue); runs 1, 2: block and split classes.
   const int cls = length <= p.t_wave ? (length <= p.alone_rows ? 0 : 3) : (length <= p.t_block ? 1 : 2);
   if (active && p.visits) p.visits[s] = 0;
+  // Register-resident softmax: its merges poll the arena's slots, which must
+  // hold zero (unpublished) when it starts. The workspace's last call
+  // recorded what it left nonzero (kCleanSlot, kDirtySlot): every thread of
+  // the launch -- the plan gives it workgroups for this beyond the segments'
+  // -- zeroes those ranges, and the part of this plan's arena beyond the
+  // extent known to be zero, before the kernel that polls them starts. A
+  // workspace as allocated is all zero.
+  if (p.arena_bytes > 0) {
+    const int64_t mark = p.counters[kCleanSlot];
+    if (mark != 0) {
+      const int64_t clean = mark == 1 ? 0 : (mark - 2 < p.arena_bytes ? mark - 2 : p.arena_bytes);
+      // The workgroups past the segments' zero the arena alone, so that the
+      // classification's workgroups are not held up by it; without such
+      // workgroups every thread takes a share.
+      const int64_t classifying = (p.b + blockDim.x - 1) / blockDim.x;
+      const bool extra = gridDim.x > classifying;
+      const int64_t first = extra ? classifying * blockDim.x : 0;
+      if (!extra || (int64_t)blockIdx.x >= classifying) {
+        const int64_t threads = (int64_t)gridDim.x * blockDim.x - first;
+        const int64_t tid = s - first;
+        // [lo, hi) widened to 16-byte words: the bytes it adds are zero
+        // already or zeroed here, and stay inside the arena (its size and
+        // the clean extent are multiples of 256). Non-temporal stores: the
+        // lines are not read again before the next kernel, and dirty L2
+        // lines would be written back at this kernel's end.
+        auto zero = [&](int64_t lo, int64_t hi) {
+          lo = lo < 0 ? 0 : lo & ~(int64_t)15;
+          hi = hi > p.arena_bytes ? p.arena_bytes : (hi + 15) & ~(int64_t)15;
+          typedef unsigned words4 __attribute__((ext_vector_type(4)));
+          words4* words = reinterpret_cast<words4*>(p.arena + lo);
+          const words4 zero4 = {0u, 0u, 0u, 0u};
+          for (int64_t i = tid; i < (hi - lo) / 16; i += threads) __builtin_nontemporal_store(zero4, words + i);
+        };
+        zero(clean, p.arena_bytes);
+        if (mark >= 2) {
+          for (int r = 0; r < kDirtyRanges; ++r) {
+            const int64_t lo = p.counters[kDirtySlot + 2 * r], hi = p.counters[kDirtySlot + 2 * r + 1];
+            if (lo < clean) zero(lo, hi < clean ? hi : clean);
+          }
+        }
+      }
+    }
+  }
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
   // Queue runs: the workgroup (kBlock threads, or kClassifyBlock for many
   // segments) reserves each class's run with one atomic (not one per wave:
@@ -549,9 +583,11 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
     const uint64_t ballot = ballots[c];
     if (ballot == 0) continue;
     const int64_t pos = run_s[c][wave] + __popcll(ballot & below);
-    if (mine) p.queue[c == 3 ? p.b - 1 - pos : c * p.b + pos] = s;
+    // A class holds at most B segments; only counters a failed call left set
+    // could reserve past that, and nothing is written there.
+    if (mine && pos < p.b) p.queue[c == 3 ? p.b - 1 - pos : c * p.b + pos] = s;
     // Register-resident softmax: whole block-class segments are items too.
-    if (mine && c == 1 && p.block_items) p.block_items[pos] = Item{start, s, (int32_t)length, -1, 0, 1};
+    if (mine && c == 1 && p.block_items && pos < p.b) p.block_items[pos] = Item{start, s, (int32_t)length, -1, 0, 1};
     if (c != 2) continue;
     // Split segments reserve ceil(L / part_rows) consecutive items. Valid
     // offsets never put more than b_split segments in the split queue;
@@ -575,8 +611,9 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
         fits = first + parts <= p.items_cap;
       }
       if (p.part_begin) p.part_begin[pos] = first;
-      // The segment's part (or chunk-group) arrivals start at zero.
-      p.seg_arrive[pos] = 0;
+      // The segment's part arrivals start at zero (streaming worker; the
+      // register-resident softmax's counters are in its arena).
+      if (p.seg_arrive) p.seg_arrive[pos] = 0;
     }
     if (p.items) {
       // Item descriptors. An allocation that does not fit the array (only

@@ -1,11 +1,11 @@
-// Op-independent kernels: pair-slot init, classification, checked offsets.
+// Op-independent kernels: counter reset, classification, checked offsets.
 #define RG_PROLOGUE_KERNELS
 #include "kernels.hpp"
 #include "table.hpp"
 
 namespace rg {
 
-const void* kernel_init() { return (const void*)&k_init; }
+const void* kernel_reset() { return (const void*)&k_reset; }
 const void* kernel_classify(int offsets_dtype) {
   return offsets_dtype ? (const void*)&k_classify<int64_t> : (const void*)&k_classify<int32_t>;
 }

@@ -17,7 +17,6 @@ struct KernelSet {
   const void* worker;            // classified schedule: wave, block and split classes in one launch
   const void* fused;             // softmax, row mapping: register-resident worker
   const void* fused_f32;         // same, storing f32 logits (scale or mask on bf16 input)
-  const void* deferred;          // softmax: re-read pass for chunks that stopped waiting
   int vec;                       // elements per vector access
   bool flat;                     // flat mapping (D < vec)
   int rpt;                       // rows per thread of `fused` (0: no fused worker)
@@ -41,12 +40,6 @@ constexpr const void* fused_kernel() {
   }
 }
 
-template <int OP, class T, class OFFT, int VEC, bool FLAT, bool MASK>
-constexpr const void* deferred_kernel() {
-  if constexpr (OP == OP_SOFTMAX && !FLAT) return (const void*)&k_softmax_deferred<T, OFFT, VEC, MASK>;
-  else return nullptr;
-}
-
 template <int OP, class T, int VEC, bool FLAT, bool MASK, bool STORE_F32>
 constexpr int fused_rpt() {
   if constexpr (OP == OP_SOFTMAX && !FLAT && (STORE_F32 || !MASK))
@@ -62,8 +55,8 @@ const KernelSet* kernels_sum(int dtype, int offsets_dtype, int geometry);
 const KernelSet* kernels_max(int dtype, int offsets_dtype, int geometry);
 const KernelSet* kernels_softmax(int dtype, int offsets_dtype, int geometry, bool mask);
 
-// Prologue and checked-mode kernels (op independent), in kernels_common.hip.
-const void* kernel_init();
+// Counter reset, classification and checked-mode kernels (op independent), in kernels_common.hip.
+const void* kernel_reset();
 const void* kernel_classify(int offsets_dtype);
 const void* kernel_offsets_init();
 const void* kernel_offsets_check(int offsets_dtype);
@@ -75,7 +68,6 @@ const void* kernel_offsets_check(int offsets_dtype);
    (const void*)&rg::k_worker<OP, T, OFFT, VEC, FLAT, MASK>,                              \
    rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, std::is_same<T, float>::value>(),              \
    rg::fused_kernel<OP, T, OFFT, VEC, FLAT, MASK, true>(),                                       \
-   rg::deferred_kernel<OP, T, OFFT, VEC, FLAT, MASK>(),                                          \
    VEC, FLAT,                                                                                    \
    rg::fused_rpt<OP, T, VEC, FLAT, MASK, std::is_same<T, float>::value>(),                       \
    rg::fused_rpt<OP, T, VEC, FLAT, MASK, true>()}
@@ -84,7 +76,7 @@ const void* kernel_offsets_check(int offsets_dtype);
 #define RG_GEOMETRIES(OP, OFFT, MASK)                                                           \
   {{RG_SET(OP, float, OFFT, 1, false, MASK), RG_SET(OP, float, OFFT, 2, false, MASK),          \
     RG_SET(OP, float, OFFT, 4, false, MASK), RG_SET(OP, float, OFFT, 4, true, MASK),           \
-    {nullptr, nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                                      \
+    {nullptr, nullptr, nullptr, nullptr, 0, false, 0, 0}},                                      \
    {RG_SET(OP, __bf16, OFFT, 1, false, MASK), RG_SET(OP, __bf16, OFFT, 2, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 4, false, MASK), RG_SET(OP, __bf16, OFFT, 8, false, MASK),        \
     RG_SET(OP, __bf16, OFFT, 8, true, MASK)}}

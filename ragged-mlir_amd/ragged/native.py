@@ -16,7 +16,7 @@ import threading
 from .errors import RuntimeUnavailable, ValidationError
 
 LIBRARY_PATH = Path(__file__).with_name("libragged_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OPS = {"sum": 0, "max": 1, "softmax": 2}
 DTYPES = {"f32": 0, "bf16": 1}
@@ -87,6 +87,7 @@ def _declare(lib: ctypes.CDLL) -> ctypes.CDLL:
         "rg_plan_create": (c_int, [vp, c_i64, c_i64, c_int, ctypes.POINTER(Plan)]),
         "rg_run": (c_int, [vp, ctypes.POINTER(Plan), vp, vp, vp, vp, vp, c_u64, vp]),
         "rg_run_static": (c_int, [vp, ctypes.POINTER(Plan), vp, vp, vp, vp, vp]),
+        "rg_test_interrupt_static": (c_int, [c_int]),
         "rg_check_offsets": (c_int, [c_int, c_int, vp, c_i64, c_i64, c_i64, c_i64, vp, vp]),
         "rg_profile_start": (c_int, [vp, c_int]),
         "rg_module_set_spin_limit": (c_int, [vp, c_i64]),

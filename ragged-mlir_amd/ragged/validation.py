@@ -37,16 +37,15 @@ def kernel_roles(spec: ProgramSpec, classes: list[str], fused: bool = False) -> 
     """Role names in launch order. The classified schedule runs classify
     (which also initialises the per-segment state of the call) and one
     worker over the wave, block and split classes (a softmax's worker also
-    normalises its split parts); with ``fused`` a softmax runs classify, an
-    init pass over the statistics slots the call's merges poll, its
-    register-resident worker, then a pass over the deferred chunks and the
-    wave class. The last kernel's last workgroup returns the workspace's
-    counters to zero."""
+    normalises its split parts); with ``fused`` a softmax runs classify and
+    its register-resident worker, which also takes the wave class and
+    re-reads the chunks that stopped waiting. The last kernel's last
+    workgroup returns the workspace's counters to zero."""
     phase = _phase(spec.op)
     if classes == ["block"] and spec.strategy == "naive":
         return [phase]
     if fused:
-        return ["classify", "init", "fused_online", "deferred_online"]
+        return ["classify", "fused_online"]
     roles = ["classify"]
     # One persistent worker drains every class; the reference's per-class
     # chains, split combine and (softmax) split normalisation run inside it.
@@ -65,7 +64,6 @@ def workspace_layout(spec: ProgramSpec, classified: bool, fused: bool = False) -
     if fused:
         workspace += [{"name": "deferred", "dtype": "i64", "shape": ["items"]},
                       {"name": "arrive", "dtype": "i32", "shape": ["items"]},
-                      {"name": "segment_arrive", "dtype": "i32", "shape": ["B_split"]},
                       {"name": "items", "dtype": "i64", "shape": ["items", 4]},
                       {"name": "block_items", "dtype": "i64", "shape": ["B", 4]},
                       {"name": "pairs", "dtype": "i64", "shape": ["items", d]},

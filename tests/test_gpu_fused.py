@@ -1,7 +1,7 @@
 """GPU tests of the register-resident softmax (k_softmax_fused): segments of
 many chunks (both merge levels), non-finite columns split across chunks, the
-bounded-wait fallback (k_softmax_deferred) forced from the host, and the
-debug queue/visit buffers."""
+bounded-wait fallback (the kernel's drain of deferred chunks) forced from the
+host, and the debug queue/visit buffers."""
 from __future__ import annotations
 
 import numpy as np
@@ -65,9 +65,10 @@ def test_nonfinite_columns_across_chunks(artifact_cache, dtype):
                                           ("f32", {"scale": 2.0})])
 def test_deferred_path_matches(artifact_cache, dtype, kwargs):
     """With a zero wait limit almost every chunk of a long segment leaves its
-    registers and is normalised by the re-read pass; the bits are those of
-    the default run (bf16 rows held as loaded, f32 rows and the f32 logits
-    of a scaled bf16 input)."""
+    registers and is normalised by the kernel's drain (a re-read; with a zero
+    limit its own wait gives up too and the last workgroup finishes it); the
+    bits are those of the default run (bf16 rows held as loaded, f32 rows
+    and the f32 logits of a scaled bf16 input)."""
     d = 128
     program = compile_softmax(artifact_cache, dtype, d, **kwargs)
     lengths = make_lengths("long_tail", 200, seed=9, total_elements=60_000)
@@ -82,8 +83,9 @@ def test_deferred_path_matches(artifact_cache, dtype, kwargs):
     finally:
         module.set_spin_limit(-1)
     check(actual, values, offsets, op="softmax", dtype=dtype, scale=kwargs.get("scale", 1.0))
-    # The re-read pass repeats the register path's arithmetic (the chunk's
-    # own reference, the same factor or lse constant): the same bits.
+    # The re-read repeats the register path's arithmetic (the same
+    # normaliser from the same fold of the segment's statistics): the same
+    # bits.
     assert np.array_equal(actual, baseline)
 
 

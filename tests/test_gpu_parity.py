@@ -311,36 +311,83 @@ def test_misaligned_workspace_rejected(artifact_cache):
           op="softmax", dtype="bf16")
 
 
+ARENA = ("pairs", "final_pairs", "arrive", "deferred")
+CLEAN_SLOT, DIRTY_SLOT, DIRTY_RANGES = 12, 14, 3
+
+
 @pytest.mark.parametrize("op,dtype,d", [("sum", "f32", 1), ("max", "f32", 128), ("softmax", "f32", 1024),
                                         ("softmax", "bf16", 128), ("softmax", "f32", 2), ("sum", "bf16", 1024)])
 def test_workspace_counters_return_to_zero(artifact_cache, op, dtype, d):
     """The workspace contract: zero before its first call; every call
     initialises the per-segment state it uses (queues, tables, arrival
-    counters, unpublished pair slots) and its last workgroup returns the
-    counters to zero. So after each call the counter region reads zero, and
-    garbage anywhere else (0xFF bytes) changes no result."""
+    counters) and its last workgroup returns the counters to zero, except
+    slot 12 and slots 14-19, the register-resident softmax's arena record:
+    such a call leaves its arena (pairs, group rows, group counters, deferred
+    list) zero but for the byte ranges of the pairs and group rows it
+    published, records its arena bytes + 2 in slot 12 and those ranges in
+    slots 14-19; any other call records 1 (arena unknown). The next call's
+    classification zeroes what the record names. So after each call the
+    counters and the arena read so; garbage (0xFF) everywhere else changes no
+    result, nor does garbage in the recorded ranges, nor garbage in the whole
+    arena recorded as unknown."""
     rng = np.random.default_rng(77 + d)
     # d >= 128: one segment long enough for the register-resident softmax's
-    # tree merge (more than 16 chunks of 256 rows), whose merged pair and
-    # group counters the call must initialise over the garbage.
+    # tree merge (more than 16 chunks of 256 rows), whose group rows and
+    # counters the call must leave as recorded.
     lengths = np.concatenate([np.zeros(30, np.int64), rng.integers(1, 40, size=400),
                               rng.integers(100, 3000, size=12), [20000 // d + 700], [12_000] if d >= 128 else []])
     lengths = rng.permutation(lengths).astype(np.int64)
     offsets = offsets_from_lengths(lengths, "i64")
     values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
     program = program_for(artifact_cache, op, dtype, d, "i64")
+    fused = bool(program.metadata["fused"])
     module = program._module(0)
     plan = program._plan(module, values.shape[0], len(lengths), "classified")
-    counters = next((offset, nbytes) for name, offset, nbytes in plan.buffers if name == "class_counts")
-    for _ in range(3):
+    spans = {name: (offset, nbytes) for name, offset, nbytes in plan.buffers}
+    counters = spans["class_counts"]
+    arena = None
+    if fused:
+        lo = min(spans[name][0] for name in ARENA if name in spans)
+        hi = max(spans[name][0] + spans[name][1] for name in ARENA if name in spans)
+        arena = (lo, (hi + 255) // 256 * 256)
+
+    def set_slot(workspace, slot, value):
+        start = counters[0] + 8 * slot
+        workspace[start:start + 8] = torch.from_numpy(np.array([value], dtype=np.int64).view(np.uint8)).to(
+            workspace.device)
+
+    for call in range(4):
         actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified")
         assert report.workspace_bytes > 0
-        assert ("ragged_0_init" in report.kernel_names) == bool(program.metadata["fused"])
+        assert len(report.kernel_names) == 2      # classify and one worker
         check(actual, values, offsets, op=op, dtype=dtype)
         torch.cuda.synchronize()
         for workspace in program._workspaces.values():
-            assert int(workspace[counters[0]:counters[0] + counters[1]].count_nonzero()) == 0
-            workspace[counters[0] + counters[1]:].fill_(255)
+            slots = workspace[counters[0]:counters[0] + counters[1]].view(torch.int64).cpu().numpy().copy()
+            if fused:
+                assert int(slots[CLEAN_SLOT]) == arena[1] - arena[0] + 2, slots[:20]
+                ranges = slots[DIRTY_SLOT:DIRTY_SLOT + 2 * DIRTY_RANGES].reshape(DIRTY_RANGES, 2)
+                assert np.all(ranges[:, 0] <= ranges[:, 1]) and ranges.min() >= 0
+                assert ranges.max() <= arena[1] - arena[0]
+                assert ranges[0, 1] > ranges[0, 0], "published direct pairs recorded"
+                image = workspace[arena[0]:arena[1]].cpu().numpy().copy()
+                for lo, hi in ranges:
+                    image[lo:hi] = 0
+                assert not image.any(), "the arena holds nonzero bytes outside the recorded ranges"
+                slots[DIRTY_SLOT:DIRTY_SLOT + 2 * DIRTY_RANGES] = 0
+            else:
+                assert int(slots[CLEAN_SLOT]) == 1, slots[:20]
+            slots[CLEAN_SLOT] = 0
+            assert not slots.any(), slots[:20]
+            workspace[(arena[1] if fused else counters[0] + counters[1]):].fill_(255)
+            if fused:
+                for lo, hi in ranges:
+                    workspace[arena[0] + lo:arena[0] + hi].fill_(255)
+                if call % 2:
+                    # Another plan's buffers over the arena: garbage there,
+                    # recorded as unknown.
+                    workspace[arena[0]:arena[1]].fill_(255)
+                    set_slot(workspace, CLEAN_SLOT, 1)
         torch.cuda.synchronize()
 
 
