@@ -278,9 +278,27 @@ __device__ __forceinline__ uint64_t load_pair_at(Rsrc r, int voffset, int soffse
   return ((uint64_t)v[1] << 32) | v[0];
 }
 
+// acc <- merge of (acc, part): the larger reference and the masses rescaled
+// to it. ACCURATE (f32 outputs) rescales with exp_split (1.25 ulp), else with
+// __expf, whose error (up to ~16 f32 ulp for large differences) is far
+// below a bf16 output's rounding.
+template <bool ACCURATE>
+__device__ __forceinline__ void merge_stats(State<OP_SOFTMAX>& acc, const State<OP_SOFTMAX>& part) {
+  if constexpr (!ACCURATE) {
+    acc.merge(part);
+  } else {
+    const float mn = fmax_nan(acc.m, part.m);
+    const float a = acc.m == neg_inf() ? acc.s : acc.s * exp_split(acc.m - mn);
+    const float b = part.m == neg_inf() ? part.s : part.s * exp_split(part.m - mn);
+    acc.s = a + b;
+    acc.m = mn;
+  }
+}
+
 // One thread's fold of `count` slots, slot_bytes apart, starting voff bytes
 // into resource r, in slot order, kBatch loads at a time; ok turns false if
 // a slot is still unpublished.
+template <bool ACCURATE>
 __device__ __forceinline__ State<OP_SOFTMAX> fold_range(Rsrc r, int voff, int count, int slot_bytes, bool& ok) {
   State<OP_SOFTMAX> acc;
   acc.init();
@@ -295,7 +313,7 @@ __device__ __forceinline__ State<OP_SOFTMAX> fold_range(Rsrc r, int voff, int co
         State<OP_SOFTMAX> part;
         part.m = pair_m(v[j]);
         part.s = pair_s(v[j]);
-        acc.merge(part);
+        merge_stats<ACCURATE>(acc, part);
       }
     }
   }
@@ -320,6 +338,7 @@ __device__ __forceinline__ int local_tid() {
 
 // A fold reads at most (count - 1) * stride + 1 slots of d pairs from base:
 // a segment's chunks or groups, far below 2^31 bytes (the plan checks it).
+template <bool ACCURATE>
 __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, int64_t stride, int d, float* lds_m,
                                            float* lds_s, uint64_t* stage) {
   const int t = local_tid();
@@ -330,7 +349,7 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
   const Rsrc pairs = make_rsrc(base, ((count - 1) * stride * d + d) * 8);
   if (r == 1) {
     for (int f = t; f < d; f += kBlock) {
-      const State<OP_SOFTMAX> st = fold_range(pairs, f * 8, (int)count, slot_bytes, ok);
+      const State<OP_SOFTMAX> st = fold_range<ACCURATE>(pairs, f * 8, (int)count, slot_bytes, ok);
       lds_m[f] = st.m;
       lds_s[f] = st.s;
     }
@@ -339,7 +358,7 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
   if (t < r * d) {
     const int part = t / d, f = t - part * d;
     const int lo = (int)(count * part / r), hi = (int)(count * (part + 1) / r);
-    const State<OP_SOFTMAX> st = fold_range(pairs, lo * slot_bytes + f * 8, hi - lo, slot_bytes, ok);
+    const State<OP_SOFTMAX> st = fold_range<ACCURATE>(pairs, lo * slot_bytes + f * 8, hi - lo, slot_bytes, ok);
     stage[t] = pack_pair(st.m, st.s);
   }
   const bool all = !block_any(!ok);
@@ -350,7 +369,7 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
       State<OP_SOFTMAX> part;
       part.m = pair_m(stage[q * d + t]);
       part.s = pair_s(stage[q * d + t]);
-      acc.merge(part);
+      merge_stats<ACCURATE>(acc, part);
     }
     lds_m[t] = acc.m;
     lds_s[t] = acc.s;
@@ -361,11 +380,12 @@ __device__ __forceinline__ bool fold_block(const uint64_t* base, int64_t count, 
 
 // fold_block until every slot is published or `ticks` of wall clock pass
 // (thread 0 decides, so the workgroup agrees); false when it gave up.
+template <bool ACCURATE>
 __device__ __forceinline__ bool poll_fold(const uint64_t* base, int64_t count, int d, int64_t ticks, float* lds_m,
                                           float* lds_s, uint64_t* stage) {
   const long long start = wall_clock64();
   for (;;) {
-    if (fold_block(base, count, 1, d, lds_m, lds_s, stage)) return true;
+    if (fold_block<ACCURATE>(base, count, 1, d, lds_m, lds_s, stage)) return true;
     bool give_up = false;
     if (threadIdx.x == 0) give_up = wall_clock64() - start >= ticks;
     if (block_any(give_up)) return false;
@@ -389,6 +409,7 @@ constexpr int kStallDivisor = 20;
 // the ticket counter stalls before the segment's last chunk is handed out
 // (the decisions are thread 0's, so the workgroup agrees); false when the
 // wait gave up.
+template <bool ACCURATE>
 __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, int d, int64_t spin_ticks,
                                           const int64_t* tickets, int64_t last_ticket, float* lds_m, float* lds_s,
                                           uint64_t* stage) {
@@ -397,7 +418,7 @@ __device__ __forceinline__ bool wait_fold(const uint64_t* base, int64_t count, i
   long long next_check = start + interval;
   int64_t seen = -1;
   for (;;) {
-    if (fold_block(base, count, 1, d, lds_m, lds_s, stage)) return true;
+    if (fold_block<ACCURATE>(base, count, 1, d, lds_m, lds_s, stage)) return true;
     bool give_up = false;
     if (threadIdx.x == 0) {
       const long long now = wall_clock64();
@@ -454,7 +475,8 @@ __device__ __forceinline__ SegmentStats segment_stats(const Params& p, int64_t i
 // fold its groups' rows directly, as a directly merged segment folds its
 // chunks' pairs: no second counter level, whose store, atomic, fold and
 // store again would sit on every chunk's wait.
-__device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t gbase, int* flag_s,
+template <bool ACCURATE>
+__device__ __forceinline__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t parts, int64_t gbase, int* flag_s,
                            float* lds_m, float* lds_s, uint64_t* stage) {
   const int t = local_tid();
   const int d = p.d;
@@ -469,7 +491,7 @@ __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t
   const bool last_in_group = *flag_s != 0;
   __syncthreads();
   if (!last_in_group) return;
-  const bool ok = poll_fold(p.pairs + gfirst * d, gsize, d, p.fold_ticks, lds_m, lds_s, stage);
+  const bool ok = poll_fold<ACCURATE>(p.pairs + gfirst * d, gsize, d, p.fold_ticks, lds_m, lds_s, stage);
   for (int f = t; f < d; f += kBlock) {
     const float nan = __uint_as_float(opaque_u32(0x7fc00000u));
     store_pair(p.final_pairs + (gbase + group) * d + f, ok ? lds_m[f] : nan, ok ? lds_s[f] : nan);
@@ -478,7 +500,7 @@ __device__ void tree_merge(const Params& p, int64_t slot, int64_t first, int64_t
 }
 
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
-__device__ void drain_and_finish(const Params& p, int64_t active, bool seen, float* lds_m, float* lds_s,
+__device__ __forceinline__ void drain_and_finish(const Params& p, int64_t active, bool seen, float* lds_m, float* lds_s,
                                  uint64_t* stage, int* flag_s, int64_t* claim_s);
 
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
@@ -488,6 +510,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
   using Store = typename std::conditional<STORE_F32, float, T>::type;
   using In = Words<T, VEC>;
   using Reg = Words<Store, VEC>;
+  // f32 outputs: merges rescale with the accurate exp, and pass 1 sums
+  // with a compensated (Kahan) add per thread, as the reference's online
+  // statistics do (ToGPU.cpp:377-387, 509-603).
+  constexpr bool kAccurate = std::is_same<T, float>::value;
   // lds: reductions, then the segment's merged max per feature, then the
   // normaliser's first constant; lds_s: the merged sum, then its second.
   __shared__ float lds[kBlock * VEC];
@@ -655,11 +681,31 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       ex[v] = ExpShift<T>(m[v] == neg_inf() ? 0.f : m[v]);
       sum[v] = 0.f;
     }
+    if constexpr (kAccurate) {
+      // Every term is in [0, 1] (or NaN): the correction is finite
+      // wherever the sum is.
+      float comp[VEC];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) {
-      if (!live(i)) continue;
+      for (int v = 0; v < VEC; ++v) comp[v] = 0.f;
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) sum[v] += ex[v](Reg::get(data[i], v));
+      for (int i = 0; i < RPT; ++i) {
+        if (!live(i)) continue;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) {
+#pragma clang fp contract(off)
+          const float y = ex[v](Reg::get(data[i], v)) - comp[v];
+          const float t = sum[v] + y;
+          comp[v] = (t - sum[v]) - y;
+          sum[v] = t;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) {
+        if (!live(i)) continue;
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) sum[v] += ex[v](Reg::get(data[i], v));
+      }
     }
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -693,16 +739,16 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       const int64_t parts = it.parts;
       for (int f = local_tid(); f < d; f += kBlock) store_pair(p.pairs + idx * d + f, own_m[f], own_s[f]);
       const bool direct = parts <= kDirect;
-      if (!direct) tree_merge(p, idx, first, parts, it.k, &flag_s, lds, lds_s, stage);
+      if (!direct) tree_merge<kAccurate>(p, idx, first, parts, it.k, &flag_s, lds, lds_s, stage);
       if (!may_wait) {
         defer = true;        // more chunks than the device surely holds at once
       } else {
         const int64_t last_ticket = ticket - it.c + parts - 1;
         const int64_t* tickets = p.counters + 4;
-        const bool ready = direct ? wait_fold(p.pairs + first * d, parts, p.d, p.spin_ticks, tickets, last_ticket,
-                                              lds, lds_s, stage)
-                                  : wait_fold(p.final_pairs + it.k * d, (parts + kGroup - 1) / kGroup, p.d,
-                                              p.spin_ticks, tickets, last_ticket, lds, lds_s, stage);
+        const bool ready = direct ? wait_fold<kAccurate>(p.pairs + first * d, parts, p.d, p.spin_ticks, tickets,
+                                                         last_ticket, lds, lds_s, stage)
+                                  : wait_fold<kAccurate>(p.final_pairs + it.k * d, (parts + kGroup - 1) / kGroup,
+                                                         p.d, p.spin_ticks, tickets, last_ticket, lds, lds_s, stage);
         defer = !ready;
         // Same thread wrote lds[f] / lds_s[f] in the fold: no barrier needed.
         if (ready) {
@@ -801,12 +847,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
 // workgroup, after every other has finished: nothing can publish later),
 // which then writes NaN, so that a lost publication is never silent.
 template <class T, int VEC, bool MASK>
-__device__ bool finish_deferred(const Params& p, int64_t idx, int64_t ticks, bool must, float* lds_m, float* lds_s,
+__device__ __forceinline__ bool finish_deferred(const Params& p, int64_t idx, int64_t ticks, bool must, float* lds_m, float* lds_s,
                                 uint64_t* stage) {
   const int t = threadIdx.x;
   const Item it = p.items[idx];
   const SegmentStats st = segment_stats(p, idx, it.c, it.parts, it.k);
-  const bool ok = poll_fold(st.base, st.count, p.d, ticks, lds_m, lds_s, stage);
+  const bool ok = poll_fold<std::is_same<T, float>::value>(st.base, st.count, p.d, ticks, lds_m, lds_s, stage);
   if (!ok && !must) return false;
   for (int f = t; f < p.d; f += kBlock) {
     const float nan = __builtin_nanf("");
@@ -846,7 +892,7 @@ __device__ bool finish_deferred(const Params& p, int64_t idx, int64_t ticks, boo
 // by then), returns the list and the counters to zero and records what the
 // call left nonzero in the arena.
 template <class T, class OffT, int VEC, int RPT, bool MASK, bool STORE_F32>
-__device__ void drain_and_finish(const Params& p, int64_t active, bool seen, float* lds_m, float* lds_s,
+__device__ __forceinline__ void drain_and_finish(const Params& p, int64_t active, bool seen, float* lds_m, float* lds_s,
                                  uint64_t* stage, int* flag_s, int64_t* claim_s) {
   const int t = threadIdx.x;
   unsigned long long* claimed = (unsigned long long*)(p.counters + kDrainSlot);

@@ -419,11 +419,14 @@ __device__ __forceinline__ int64_t active_workgroups(int64_t work) {
 // on MI355X): workgroup w at lane w % kTicketLanes (the done lanes,
 // kTicketStride apart after the ticket lanes), the last of each lane at
 // counters[kDoneSlot]. The last workgroup may still use the workspace; it
-// then calls reset_counters.
+// then calls reset_counters. With `drain` the count is a release at agent
+// scope (stores complete, then an L2 writeback, as in split_part) and the
+// last workgroup acquires: what the others wrote is visible to it.
 __device__ __forceinline__ bool last_out(const Params& p, int* flag_s, int64_t active, bool drain) {
   if (drain) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): this workgroup's stores are complete
   __syncthreads();
   if (threadIdx.x == 0) {
+    if (drain) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const unsigned count = (unsigned)active;
     bool last = false;
     if (count <= kDirectDone) {
@@ -439,6 +442,7 @@ __device__ __forceinline__ bool last_out(const Params& p, int* flag_s, int64_t a
       if (atomicAdd(lane_counter, 1ull) == in_lane - 1)
         last = atomicAdd((unsigned long long*)(p.counters + kDoneSlot), 1ull) == lanes - 1;
     }
+    if (last && drain) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     *flag_s = last ? 1 : 0;
   }
   __syncthreads();

@@ -124,6 +124,25 @@ __device__ __forceinline__ void fold_residues(float (&x)[VEC], int d) {
   }
 }
 
+// A softmax column sum of exp terms in [0, 1]: compensated (Kahan) for f32
+// outputs, as the reference's statistics are (ToGPU.cpp:377-387, 509-603),
+// plain for bf16 outputs (far below their rounding).
+template <class T>
+struct ExpSum {
+  float s = 0.f, c = 0.f;
+  __device__ void add(float e) {
+    if constexpr (std::is_same<T, float>::value) {
+#pragma clang fp contract(off)
+      const float y = e - c;
+      const float t = s + y;
+      c = (t - s) - y;
+      s = t;
+    } else {
+      s += e;
+    }
+  }
+};
+
 // Vectors a lane holds in registers for a short flat segment (48 floats).
 template <int VEC>
 constexpr int kLaneVectors = 48 / VEC;
@@ -144,6 +163,7 @@ __device__ __forceinline__ void lane_softmax_held(const Params& p, int64_t lo, i
     return j0 + u <= j1 && e >= lo && e < hi;
   };
   float m[VEC], ref[VEC], s[VEC], inv[VEC];
+  ExpSum<T> acc[VEC];
 #pragma unroll
   for (int c = 0; c < VEC; ++c) m[c] = neg_inf();
 #pragma unroll
@@ -153,18 +173,17 @@ __device__ __forceinline__ void lane_softmax_held(const Params& p, int64_t lo, i
   }
   fold_residues<true, VEC>(m, d);
 #pragma unroll
-  for (int c = 0; c < VEC; ++c) {
-    ref[c] = m[c] == neg_inf() ? 0.f : m[c];
-    s[c] = 0.f;
-  }
+  for (int c = 0; c < VEC; ++c) ref[c] = m[c] == neg_inf() ? 0.f : m[c];
 #pragma unroll
   for (int u = 0; u < K; ++u) {
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       x[u][c] = exp_out<T>(x[u][c] - ref[c]);
-      s[c] += inside(u, c) ? x[u][c] : 0.f;
+      acc[c].add(inside(u, c) ? x[u][c] : 0.f);
     }
   }
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) s[c] = acc[c].s;
   fold_residues<false, VEC>(s, d);
 #pragma unroll
   for (int c = 0; c < VEC; ++c) inv[c] = fast_exp(m[c] - m[c]) / s[c];   // 1 / s, or NaN for an all -inf column
@@ -216,18 +235,18 @@ __device__ __forceinline__ void lane_softmax(const Params& p, int64_t lo, int64_
   });
   fold_residues<true, VEC>(m, d);
   float ref[VEC], s[VEC];
+  ExpSum<T> acc[VEC];
 #pragma unroll
-  for (int c = 0; c < VEC; ++c) {
-    ref[c] = m[c] == neg_inf() ? 0.f : m[c];
-    s[c] = 0.f;
-  }
+  for (int c = 0; c < VEC; ++c) ref[c] = m[c] == neg_inf() ? 0.f : m[c];
   pass([&](int64_t j, const float (&x)[VEC]) {
 #pragma unroll
     for (int c = 0; c < VEC; ++c) {
       const int64_t e = j * VEC + c;
-      if (e >= lo && e < hi) s[c] += exp_out<T>(x[c] - ref[c]);
+      if (e >= lo && e < hi) acc[c].add(exp_out<T>(x[c] - ref[c]));
     }
   });
+#pragma unroll
+  for (int c = 0; c < VEC; ++c) s[c] = acc[c].s;
   fold_residues<false, VEC>(s, d);
   float inv[VEC];
 #pragma unroll
@@ -292,12 +311,10 @@ __device__ __forceinline__ void group_segment(const Params& p, int64_t s, int64_
       }
     };
     if constexpr (OP == OP_SOFTMAX) {
-      float m[VEC], sum[VEC], ref[VEC], inv[VEC];
+      float m[VEC], ref[VEC], inv[VEC];
+      ExpSum<T> sum[VEC];
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) {
-        m[v] = neg_inf();
-        sum[v] = 0.f;
-      }
+      for (int v = 0; v < VEC; ++v) m[v] = neg_inf();
       rows([&](int64_t, const float (&x)[VEC]) {
 #pragma unroll
         for (int v = 0; v < VEC; ++v) m[v] = fmax_nan(m[v], x[v]);
@@ -306,10 +323,10 @@ __device__ __forceinline__ void group_segment(const Params& p, int64_t s, int64_
       for (int v = 0; v < VEC; ++v) ref[v] = m[v] == neg_inf() ? 0.f : m[v];
       rows([&](int64_t, const float (&x)[VEC]) {
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) sum[v] += exp_out<T>(x[v] - ref[v]);
+        for (int v = 0; v < VEC; ++v) sum[v].add(exp_out<T>(x[v] - ref[v]));
       });
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) inv[v] = fast_exp(m[v] - m[v]) / sum[v];   // NaN for an all -inf column
+      for (int v = 0; v < VEC; ++v) inv[v] = fast_exp(m[v] - m[v]) / sum[v].s;   // NaN for an all -inf column
       T* out = static_cast<T*>(p.out);
       rows([&](int64_t r, const float (&x)[VEC]) {
         float y[VEC];
@@ -381,9 +398,22 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
   const int tiles = FLAT ? 1 : tiles_of<VEC>(p.d, kBlock);
   const int64_t first = p.part_begin[k];
   const int64_t stop = first + all_parts < p.items_cap ? first + all_parts : p.items_cap;
+  //
+  // Ordering (the LLVM AMDGPU memory model for gfx942/gfx950): the arrival
+  // is a release at agent scope -- every thread's stores complete
+  // (s_waitcnt vmcnt(0)) before the barrier, then thread 0's release fence
+  // (buffer_wbl2 sc1: the XCD's L2 written back) precedes the atomic -- and
+  // the last arriver acquires at agent scope (buffer_inv sc1) before the
+  // barrier after which its threads read the other parts' partials. Parts
+  // run on any XCD, each with its own L2.
   __builtin_amdgcn_s_waitcnt(0x0F70);
   __syncthreads();
-  if (t == 0) *flag_s = atomicAdd(p.seg_arrive + k, 1) == (stop - first) * tiles - 1;
+  if (t == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const bool last = atomicAdd(p.seg_arrive + k, 1) == (stop - first) * tiles - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    *flag_s = last;
+  }
   __syncthreads();
   const bool last = *flag_s != 0;
   __syncthreads();
@@ -429,10 +459,14 @@ __device__ __forceinline__ void split_part(const Params& p, int64_t item, int ti
     if (p.visits && t == 0) atomicAdd(p.visits + s, 1);
   } else {
     // The statistics are complete once every thread's stores are: release
-    // the segment's parts to their normalisation (normalize_part).
+    // the segment's parts to their normalisation (normalize_part), with
+    // the same agent-scope release as the arrival above.
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
-    if (t == 0) __hip_atomic_store(p.seg_arrive + k, kStatsReady, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      __hip_atomic_store(p.seg_arrive + k, kStatsReady, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -460,6 +494,9 @@ __device__ __forceinline__ bool normalize_part(const Params& p, int64_t item, in
         }
         __builtin_amdgcn_s_sleep(2);
       }
+      // Acquire at agent scope: the statistics read below were released
+      // before the flag.
+      if (ready) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     if (block_any(!ready)) return false;
   }

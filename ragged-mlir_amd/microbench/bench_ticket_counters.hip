@@ -2,7 +2,7 @@
 // tickets from 16 interleaved counters and k_classify reserving one run of
 // queue positions per class and workgroup. Not part of the library: build
 // and run it on its own,
-//   hipcc --offload-arch=gfx950 -O3 ragged-mlir_amd/csrc/bench_ticket_counters.hip -o /tmp/tickets && /tmp/tickets
+//   hipcc --offload-arch=gfx950 -O3 ragged-mlir_amd/microbench/bench_ticket_counters.hip -o /tmp/tickets && /tmp/tickets
 // Each of `grid` workgroups (256 threads) takes tickets until `total` are
 // handed out: thread 0 adds 1 to counter (blockIdx % lanes), and the ticket
 // is (old value) * lanes + lane, as in k_worker. Counters sit 256 bytes

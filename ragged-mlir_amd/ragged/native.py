@@ -184,6 +184,13 @@ def uses_fused(spec: Spec) -> bool:
     return status == 1
 
 
+def interrupt_static(launches: int) -> None:
+    """Test control (``rg_test_interrupt_static``): the next ``run_static``
+    stops after ``launches`` launches of its plan and fails as a launch error
+    would; -1 turns it off."""
+    _check(library().rg_test_interrupt_static(int(launches)), "rg_test_interrupt_static")
+
+
 def device_clock_khz(device: int = 0) -> int:
     """Rate of the device wall clock (the timeline records' ticks), in kHz."""
     khz = ctypes.c_int64(0)

@@ -156,9 +156,12 @@ def recorded_cases():
 def test_reference_recorded_error_statistics(artifact_cache, case):
     """The reference recorded, for these exact inputs, every method's oracle
     error (results/bench/runs/compare/*/seed-711/rep-0/results.json).
-    Max must be exact as there; sum and softmax must stay within 1.5x the
-    worst of the reference's measured methods, and bf16 softmax (whose error
-    is the output's one rounding) within 1.05x the reference's own."""
+    Max must be exact as there. The register-resident f32 softmax (every
+    output exp(x - M) * (1 / S) from the input, its statistics summed with
+    compensation and merged with the accurate exp) stays within the worst of
+    the reference's measured methods; the streaming schedules' sum and
+    softmax within 1.5x of it; bf16 softmax (whose error is the output's one
+    rounding) within 1.05x the reference's own."""
     lengths = make_lengths(case["distribution"], case["segments"], seed=case["seed"],
                            total_elements=case["total_elements"], mean_length=case["mean_length"])
     offsets = offsets_from_lengths(lengths, case["offsets_dtype"])
@@ -170,16 +173,23 @@ def test_reference_recorded_error_statistics(artifact_cache, case):
     methods = case["methods"]
     envelope = max(m["max_fraction_of_tolerance"] for m in methods.values())
     expectation = oracle.Expectation(quantized(values, dtype), offsets, operation=op, input_dtype=dtype)
+    results = []
     for select in ("auto", "classified", "naive"):
         actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select=select)
         stats = expectation.check(actual)
-        print(f"{case['source']} {select}: ours {stats['max_abs_error']:.3g} / {stats['max_fraction_of_tolerance']:.3g}"
+        register_resident = bool(program.metadata["fused"]) and report.selected == "classified"
+        print(f"{case['source']} {select} ({report.selected}{', register-resident' if register_resident else ''}): "
+              f"ours {stats['max_abs_error']:.3g} / {stats['max_fraction_of_tolerance']:.3g}"
               f", reference ragged-auto {methods['ragged-auto']['max_abs_error']:.3g} / "
               f"{methods['ragged-auto']['max_fraction_of_tolerance']:.3g}, envelope {envelope:.3g}")
+        results.append((stats, register_resident))
+    for stats, register_resident in results:
         assert stats["finite_values"] == methods["ragged-auto"]["finite_values"]
         assert stats["nan_values"] == methods["ragged-auto"]["nan_values"]
         if op == "max":
             assert stats["max_abs_error"] == 0.0
+        elif op == "softmax" and dtype == "f32" and register_resident:
+            assert stats["max_fraction_of_tolerance"] <= envelope + 1e-9
         else:
             assert stats["max_fraction_of_tolerance"] <= 1.5 * envelope + 1e-9
         if op == "softmax" and dtype == "bf16":

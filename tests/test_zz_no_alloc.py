@@ -87,3 +87,42 @@ def test_plan_beyond_the_static_workspace_is_rejected():
     torch.cuda.synchronize()
     assert bool(torch.all(out == 7.0))
     module.close()
+
+
+@pytest.mark.parametrize("op,dtype,d,offsets_dtype,distribution,first,second", CASES[:2])
+def test_static_call_interrupted_after_a_launch_recovers(op, dtype, d, offsets_dtype, distribution, first, second):
+    """A static call that fails after its first launch (the classification
+    ran and counted; nothing returned the counters to zero) leaves the
+    device's static workspace marked. The next static call first returns
+    the counters to zero with a one-workgroup kernel: its result equals
+    rg_run's on a fresh workspace, bit for bit."""
+    spec = native.make_spec(op, dtype, offsets_dtype, d)
+    module = native.NativeModule(0, spec)
+    tdtype = torch.bfloat16 if dtype == "bf16" else torch.float32
+    view = torch.int16 if dtype == "bf16" else torch.int32
+    stream = torch.cuda.current_stream().cuda_stream
+    values, offsets = inputs(distribution, first, d, offsets_dtype, seed=71)
+    b = len(offsets) - 1
+    plan = module.plan(first, b, "classified")
+    x = torch.from_numpy(values).to(DEVICE).to(tdtype)
+    off = torch.from_numpy(offsets).to(DEVICE)
+    out_rows = first if op == "softmax" else b
+    expected = torch.full((out_rows, d), float("nan"), dtype=tdtype, device=DEVICE)
+    actual = torch.full_like(expected, float("nan"))
+    native.interrupt_static(1)
+    try:
+        with pytest.raises(RuntimeError, match="interrupted after 1 launches"):
+            module.run_static(plan, x.data_ptr(), off.data_ptr(), actual.data_ptr(), None, stream)
+    finally:
+        native.interrupt_static(-1)
+    torch.cuda.synchronize()
+    workspace = torch.zeros((int(plan.workspace_bytes),), dtype=torch.uint8, device=DEVICE)
+    module.run(plan, x.data_ptr(), off.data_ptr(), expected.data_ptr(), None, workspace.data_ptr(),
+               int(plan.workspace_bytes), stream)
+    for _ in range(2):
+        actual.fill_(float("nan"))
+        module.run_static(plan, x.data_ptr(), off.data_ptr(), actual.data_ptr(), None, stream)
+        torch.cuda.synchronize()
+        assert torch.equal(actual.view(view), expected.view(view)), "a static call after the failed one differs"
+    check(actual.float().cpu().numpy().astype(np.float64), values, offsets, op=op, dtype=dtype)
+    module.close()
