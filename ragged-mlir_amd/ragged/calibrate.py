@@ -456,6 +456,22 @@ def fit(records: list[dict]) -> dict:
     return data
 
 
+def leave_one_suite_out(files: dict[str, list[dict]]) -> dict:
+    """Each measurement file held out in turn: the model form fitted on the
+    others pooled, scored on it warm and cold (the share of choices within
+    3% of the faster schedule, as run(select="auto") makes them), and the
+    means over the files."""
+    report = {}
+    for held in files:
+        model = CostModel.from_dict(fit([r for name, records in files.items() if name != held for r in records]))
+        report[held] = {"cases": len(files[held]), "within_3pct": evaluate(model, files[held])["share"],
+                        "within_3pct_cold": evaluate(model, files[held], cold=True)["share"]}
+    report["mean_within_3pct"] = round(float(np.mean([r["within_3pct"] for r in report.values()])), 4)
+    report["mean_within_3pct_cold"] = round(float(np.mean([r["within_3pct_cold"] for r in report.values()
+                                                           if isinstance(r, dict)])), 4)
+    return report
+
+
 def transfer(train: list[dict], heldout: list[dict], shipped: CostModel) -> tuple[dict, dict]:
     """(refitted model file, report): the refit on ``train`` and, on
     ``heldout``, the share within 3% of the faster schedule for the shipped
@@ -485,6 +501,9 @@ def main(argv=None) -> int:
     f.add_argument("--heldout", type=Path, help="held-out measurements to evaluate the fit on (recorded only)")
     f.add_argument("--check", type=Path, action="append", default=[],
                    help="further measurements to score the fit on (recorded only; repeat)")
+    f.add_argument("--loso", action="store_true",
+                   help="also record the leave-one-suite-out scores over the train files")
+    f.add_argument("--heldout-commit", help="commit that froze the held-out suite's definition (recorded)")
     e = sub.add_parser("evaluate")
     e.add_argument("results", type=Path)
     e.add_argument("--model", type=Path)
@@ -518,6 +537,11 @@ def main(argv=None) -> int:
             if all("us_cold" in r for r in heldout):
                 cold = evaluate(CostModel.from_dict(data), heldout, cold=True)
                 data["calibration"]["heldout_within_3pct_cold"] = cold["share"]
+            if args.heldout_commit:
+                data["calibration"]["heldout_definition_commit"] = args.heldout_commit
+        if args.loso:
+            data["calibration"]["leave_one_suite_out"] = leave_one_suite_out(
+                {path.stem: load(path) for path in args.results})
         for path in args.check:
             records = load(path)
             entry = {"cases": len(records), "within_3pct": evaluate(CostModel.from_dict(data), records)["share"]}

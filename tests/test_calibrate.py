@@ -156,23 +156,25 @@ def test_evaluate_counts_within_three_percent():
 
 
 TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5", "heldout6",
-                "heldout7")
+                "heldout7", "heldout8")
+HELDOUT = "heldout9"
+# The commit that froze heldout9's definition (and pinned its first keys)
+# before any of it was measured.
+HELDOUT_COMMIT = "ff93b6565e367dfb282bc4d6c6ad1fe9b0e2a7d6"
 
 
 def test_shipped_model_records_its_heldout_scores():
     """The committed cost model is the fit of the committed MI355X
-    measurements of every suite but heldout8, pooled (refitting reproduces
+    measurements of every suite but heldout9, pooled (refitting reproduces
     its coefficients and margins), all measured with the library whose
     sha256 it records; its choices, as run(select="auto") makes them, are
-    scored on heldout8 (frozen before the fit, disjoint shapes, scored once)
-    warm and cold exactly as recorded. Every measured case passed the
-    sampled correctness gate."""
+    scored on heldout9 (its definition committed before any of it was
+    measured, disjoint shapes, scored once) warm and cold exactly as
+    recorded, and its leave-one-suite-out scores over the train suites are
+    recorded as recomputed. Every measured case passed the sampled
+    correctness gate."""
     base = Path(calibrate.__file__).with_name("calibration")
-    # heldout9 is frozen ahead of its measurement (test_suites_are_fixed_and_disjoint
-    # pins it); until then it has no file.
-    measured = [name for name in calibrate.SUITES if (base / f"{name}.jsonl").exists()]
-    assert set(calibrate.SUITES) - set(measured) <= {"heldout9"}
-    files = {name: calibrate.load(base / f"{name}.jsonl") for name in measured}
+    files = {name: calibrate.load(base / f"{name}.jsonl") for name in calibrate.SUITES}
     for name, records in files.items():
         assert {r["key"] for r in records} == {c.key for c in calibrate.suite(name)}, name
         assert all(0.0 <= g <= 1.0 for r in records for g in r["gate"].values()), name
@@ -180,10 +182,11 @@ def test_shipped_model_records_its_heldout_scores():
     model = CostModel.load()
     shas = {r["library_sha256"] for records in files.values() for r in records}
     assert shas == {model.calibration["library_sha256"]}
-    heldout = files["heldout8"]
+    heldout = files[HELDOUT]
     warm, cold = calibrate.evaluate(model, heldout), calibrate.evaluate(model, heldout, cold=True)
     assert warm["cases"] == cold["cases"] == 150
-    assert model.calibration["heldout_file"] == "heldout8.jsonl"
+    assert model.calibration["heldout_file"] == f"{HELDOUT}.jsonl"
+    assert model.calibration["heldout_definition_commit"] == HELDOUT_COMMIT
     assert model.calibration["train_file"] == " + ".join(f"{name}.jsonl" for name in TRAIN_SUITES)
     assert model.calibration["heldout_within_3pct"] == warm["share"]
     assert model.calibration["heldout_within_3pct_cold"] == cold["share"]
@@ -192,6 +195,8 @@ def test_shipped_model_records_its_heldout_scores():
         for schedule, coefficients in schedules.items():
             assert coefficients == pytest.approx(list(model.coefficients[fam][schedule]), rel=1e-4, abs=1e-6)
     assert refit["margins"] == model.margins
+    loso = calibrate.leave_one_suite_out({name: files[name] for name in TRAIN_SUITES})
+    assert loso == model.calibration["leave_one_suite_out"]
 
 
 def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp_path):
@@ -201,7 +206,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     held-out share; the CLI writes the refit and prints the report."""
     directory = Path(calibrate.__file__).with_name("calibration")
     train = [r for name in TRAIN_SUITES for r in calibrate.load(directory / f"{name}.jsonl")]
-    heldout = calibrate.load(directory / "heldout8.jsonl")
+    heldout = calibrate.load(directory / f"{HELDOUT}.jsonl")
     shipped = CostModel.load()
     data, report = calibrate.transfer(train, heldout, shipped)
     assert data["coefficients"] == json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())[
@@ -213,7 +218,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     out = tmp_path / "refit.json"
     pooled = tmp_path / "train_pooled.jsonl"
     pooled.write_text("".join(json.dumps(record) + "\n" for record in train))
-    assert calibrate.main(["transfer", str(pooled), str(directory / "heldout8.jsonl"), "--out", str(out)]) == 0
+    assert calibrate.main(["transfer", str(pooled), str(directory / f"{HELDOUT}.jsonl"), "--out", str(out)]) == 0
     assert json.loads(out.read_text())["coefficients"] == data["coefficients"]
 
 
