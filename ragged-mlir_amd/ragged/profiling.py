@@ -17,6 +17,9 @@ summarises Nsight Compute metrics) for rocprofv3 output on gfx950:
   FETCH_SIZE / WRITE_SIZE runs and an occupancy run (OccupancyPercent,
   MeanOccupancyPerCU, VALUBusy, MemUnitStalled) plus the algorithmic bytes a
   ``bench.py --details`` file records per kernel role.
+* ``dispatches``: a kernel trace of back-to-back calls of a two-launch
+  schedule (classification, then the main kernel) reduced per timed pass to
+  the time per call, each kernel's duration and the gaps between them;
 * ``item_timeline``: the register-resident softmax's item trace (one call
   under ``rg_module_set_trace``, ``bench.py --timeline``) reduced to each
   item class's phase durations and workgroup time, how many workgroups were
@@ -221,6 +224,50 @@ def report(stats_db: Path, fetch_db: Path, write_db: Path, occupancy_db: Path, f
     return lines
 
 
+def dispatch_times(path: Path) -> list[tuple[str, int, int]]:
+    """(kernel, start ns, end ns) of every dispatch of a kernel-trace
+    database, in start order."""
+    try:
+        rows = _query(path, "select name, start, end from kernels order by start")
+    except sqlite3.OperationalError:
+        rows = _query(path, "select s.kernel_name, d.start, d.end from rocpd_kernel_dispatch d "
+                            "join rocpd_info_kernel_symbol s on d.kernel_id = s.id order by d.start")
+    return [(short_name(name), int(start), int(end)) for name, start, end in rows]
+
+
+def call_passes(dispatches: list[tuple[str, int, int]], first: str, last: str, skip: int, steps: int,
+                passes: int) -> list[dict[str, float]]:
+    """Calls of a two-launch schedule: each dispatch of a kernel matching
+    ``first`` followed by the next one matching ``last`` (other kernels are
+    ignored). After ``skip`` calls, ``passes`` runs of ``steps`` calls each:
+    per run, the time per call (first start to last end over the run,
+    divided by ``steps``), the mean duration of both kernels, the mean gap
+    from the first kernel's end to the second's start, and the mean gap from
+    a call's end to the next call's start within the run (µs)."""
+    calls, pending = [], None
+    for name, start, end in dispatches:
+        if re.search(first, name):
+            pending = (start, end)
+        elif re.search(last, name) and pending is not None:
+            calls.append((*pending, start, end))
+            pending = None
+    out = []
+    for k in range(passes):
+        run = calls[skip + k * steps: skip + (k + 1) * steps]
+        if len(run) < steps:
+            raise ValueError(f"pass {k}: {len(run)} of {steps} calls in the trace ({len(calls)} calls in all)")
+        mean = lambda values: sum(values) / len(values) / 1e3
+        out.append({"calls": steps,
+                    "per_call_us": (run[-1][3] - run[0][0]) / steps / 1e3,
+                    "first_us": mean([c[1] - c[0] for c in run]),
+                    "gap_first_last_us": mean([c[2] - c[1] for c in run]),
+                    "last_us": mean([c[3] - c[2] for c in run]),
+                    "last_min_us": min(c[3] - c[2] for c in run) / 1e3,
+                    "last_max_us": max(c[3] - c[2] for c in run) / 1e3,
+                    "gap_next_call_us": mean([run[j + 1][0] - run[j][3] for j in range(steps - 1)]) if steps > 1 else 0.0})
+    return out
+
+
 TIMELINE_CLASSES = {0: "whole", 1: "direct", 2: "tree"}
 TIMELINE_PHASES = ("load_max", "exp_sum", "merge", "store")
 
@@ -335,6 +382,13 @@ def main(argv: list[str] | None = None) -> int:
     t.add_argument("--out", type=Path, help="also write the result as JSON here")
     r = sub.add_parser("resources", help="VGPR/AGPR/SGPR/LDS/scratch per kernel of a kernel-trace database")
     r.add_argument("db", type=Path)
+    g = sub.add_parser("dispatches", help="per timed pass: time per call, both kernels and the gaps between them")
+    g.add_argument("db", type=Path, help="--kernel-trace database")
+    g.add_argument("--first", default="k_classify", help="regex of a call's first kernel")
+    g.add_argument("--last", default="k_softmax_fused|k_worker", help="regex of a call's second kernel")
+    g.add_argument("--skip", type=int, required=True, help="calls before the first timed pass")
+    g.add_argument("--steps", type=int, required=True, help="calls per timed pass")
+    g.add_argument("--passes", type=int, default=2)
     m = sub.add_parser("report", help="markdown per-kernel table of one workload")
     m.add_argument("--stats", type=Path, required=True, help="--kernel-trace --stats database")
     m.add_argument("--fetch", type=Path, required=True)
@@ -350,6 +404,14 @@ def main(argv: list[str] | None = None) -> int:
     args = parser.parse_args(argv)
     if args.command == "resources":
         print(json.dumps(kernel_resources(args.db), indent=1))
+        return 0
+    if args.command == "dispatches":
+        rows = call_passes(dispatch_times(args.db), args.first, args.last, args.skip, args.steps, args.passes)
+        print("| pass | calls | per call µs | first kernel µs | gap µs | second kernel µs (min-max) | gap to next call µs |")
+        print("|---|---:|---:|---:|---:|---:|---:|")
+        for k, r in enumerate(rows):
+            print(f"| {k + 1} | {r['calls']} | {r['per_call_us']:.1f} | {r['first_us']:.2f} | {r['gap_first_last_us']:.2f} | "
+                  f"{r['last_us']:.2f} ({r['last_min_us']:.1f}-{r['last_max_us']:.1f}) | {r['gap_next_call_us']:.2f} |")
         return 0
     if args.command == "report":
         factor = copy_factor(args.copy_fetch, args.copy_write, args.copy_bytes, args.copy_kernel)

@@ -144,3 +144,37 @@ def test_item_timeline_known_answers():
     # Items live and merging at t = 4, 12, 20, 28.
     assert summary["profile"] == [[8, 1], [5, 5], [5, 2], [2, 2]]
     assert profiling.item_timeline([[0] * 8], clock_khz=1000, part_rows=256) == {"items": 0}
+
+
+def test_call_passes_known_answers(tmp_path, capsys):
+    """Two passes of two calls each after one skipped call, from a database
+    in the rocpd layout (dispatch and symbol tables, no kernels view), with a
+    foreign kernel in between that is ignored; values in ns, hand-computed."""
+    db = tmp_path / "trace.db"
+    connection = sqlite3.connect(db)
+    connection.execute("create table rocpd_info_kernel_symbol (id integer, kernel_name text)")
+    connection.execute("create table rocpd_kernel_dispatch (kernel_id integer, start integer, end integer)")
+    connection.executemany("insert into rocpd_info_kernel_symbol values (?, ?)",
+                           [(1, "rg::k_classify<long>(rg::Params)"),
+                            (2, "void rg::k_softmax_fused<__bf16, long, 8, 16, false, false>(rg::Params)"),
+                            (3, "at::native::copy_kernel")])
+    dispatches = [(1, 0, 10_000), (2, 10_000, 400_000),                          # skipped call
+                  (1, 400_000, 411_000), (2, 411_000, 890_000),                  # pass 1: back to back
+                  (1, 890_000, 901_000), (2, 901_000, 1_380_000),
+                  (3, 1_380_000, 1_390_000),                                     # foreign kernel
+                  (1, 1_400_000, 1_410_000), (2, 1_416_000, 1_876_000),          # pass 2: gaps of 6 and 10 µs
+                  (1, 1_886_000, 1_896_000), (2, 1_902_000, 2_362_000)]
+    connection.executemany("insert into rocpd_kernel_dispatch values (?, ?, ?)", dispatches)
+    connection.commit()
+    connection.close()
+    rows = profiling.call_passes(profiling.dispatch_times(db), "k_classify", "k_softmax_fused", 1, 2, 2)
+    assert rows[0] == {"calls": 2, "per_call_us": 490.0, "first_us": 11.0, "gap_first_last_us": 0.0,
+                       "last_us": 479.0, "last_min_us": 479.0, "last_max_us": 479.0, "gap_next_call_us": 0.0}
+    assert rows[1] == {"calls": 2, "per_call_us": 481.0, "first_us": 10.0, "gap_first_last_us": 6.0,
+                       "last_us": 460.0, "last_min_us": 460.0, "last_max_us": 460.0, "gap_next_call_us": 10.0}
+    with pytest.raises(ValueError, match="pass 1"):
+        profiling.call_passes(profiling.dispatch_times(db), "k_classify", "k_softmax_fused", 1, 3, 2)
+    assert profiling.main(["dispatches", str(db), "--skip", "1", "--steps", "2"]) == 0
+    out = capsys.readouterr().out
+    assert "| 1 | 2 | 490.0 | 11.00 | 0.00 | 479.00 (479.0-479.0) | 0.00 |" in out
+    assert "| 2 | 2 | 481.0 | 10.00 | 6.00 | 460.00 (460.0-460.0) | 10.00 |" in out
