@@ -114,6 +114,8 @@ bool add_ok(int64_t a, int64_t b, int64_t* out) { return !__builtin_add_overflow
 constexpr uint64_t kStaticScratchBytes = RG_STATIC_WORKSPACE_BYTES;
 constexpr int kMaxDevices = 64;
 constexpr size_t kScratchCounterBytes = (size_t)rg::kTicketStride * 8 * (1 + 2 * rg::kTicketLanes);
+static_assert(kStaticScratchBytes % 256 == 0 && kStaticScratchBytes >= kScratchCounterBytes,
+              "RG_STATIC_WORKSPACE_BYTES: a multiple of 256 bytes that holds at least the counters");
 std::mutex g_scratch_mutex;
 void* g_scratch[kMaxDevices];          // device address of `scratch` on each device, or null
 // A call on the device's static workspace failed after it had launched
