@@ -851,9 +851,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
 // appear in time it returns false having written nothing -- unless `must` (the last
 // workgroup, after every other has finished: nothing can publish later),
 // which then writes NaN, so that a lost publication is never silent.
-template <class T, int VEC, bool MASK>
+template <class T, int VEC, int RPT, bool MASK, bool STORE_F32>
 __device__ __forceinline__ bool finish_deferred(const Params& p, int64_t idx, int64_t ticks, bool must, float* lds_m, float* lds_s,
                                 uint64_t* stage) {
+  using Store = typename std::conditional<STORE_F32, float, T>::type;
+  using In = Words<T, VEC>;
+  using Reg = Words<Store, VEC>;
   const int t = threadIdx.x;
   const Item it = p.items[idx];
   const SegmentStats st = segment_stats(p, idx, it.c, it.parts, it.k);
@@ -867,18 +870,71 @@ __device__ __forceinline__ bool finish_deferred(const Params& p, int64_t idx, in
   }
   __syncthreads();
   const RowGeo g = row_geo<VEC>(p.d, kBlock, t, 0);
-  if (g.active) {
-    Normalizer<T> norm[VEC];
+  if constexpr (MASK) {
+    // Masked logits: one row step at a time (holding the mask's words as
+    // well would spill the register path's rows).
+    if (g.active) {
+      Normalizer<T> norm[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) norm[v] = Normalizer<T>(lds_m[g.feature + v], lds_s[g.feature + v]);
-    T* out = static_cast<T*>(p.out);
-    for (int64_t r = it.start + g.row_lane; r < it.start + it.rows; r += g.rows_step) {
-      float x[VEC];
-      load_input<T, VEC, MASK>(p, r * p.d + g.feature, x);
+      for (int v = 0; v < VEC; ++v) norm[v] = Normalizer<T>(lds_m[g.feature + v], lds_s[g.feature + v]);
+      T* out = static_cast<T*>(p.out);
+      for (int64_t r = it.start + g.row_lane; r < it.start + it.rows; r += g.rows_step) {
+        float x[VEC];
+        load_input<T, VEC, MASK>(p, r * p.d + g.feature, x);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) x[v] = norm[v](x[v]);
-      Elem<T>::template store<VEC>(out + r * p.d + g.feature, x);
+        for (int v = 0; v < VEC; ++v) x[v] = norm[v](x[v]);
+        Elem<T>::template store<VEC>(out + r * p.d + g.feature, x);
+      }
     }
+    if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
+    __syncthreads();
+    return true;
+  }
+  // The chunk's rows as the register path holds them (the same row
+  // mapping, every load in flight at once, the same input transform), so
+  // each output takes the register path's arithmetic and bits.
+  const bool wave_rows = g.lpr <= kWave;
+  const int rstep = wave_rows ? kWave / g.lpr : g.rows_step;
+  const int row0 = wave_rows ? (t / kWave) * RPT * rstep + (t % kWave) / g.lpr : g.row_lane;
+  const int wave_row0 = wave_rows ? __builtin_amdgcn_readfirstlane((t / kWave) * RPT * rstep) : 0;
+  const int voff = g.active ? (row0 * p.d + g.feature) * (int)sizeof(T) : kOutOfRange;
+  const int step = rstep * p.d * (int)sizeof(T);
+  const int64_t elems = (int64_t)it.rows * p.d;
+  const Rsrc in = make_rsrc(static_cast<const T*>(p.values) + it.start * p.d, elems * (int64_t)sizeof(T));
+  uint32_t data[RPT][Reg::kCount];
+  if constexpr (!STORE_F32) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) buffer_load<In::kBytes>(in, voff + i * step, 0, data[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+#pragma clang fp contract(off)
+      uint32_t raw[In::kCount];
+      buffer_load<In::kBytes>(in, voff + i * step, 0, raw);
+      float x[VEC];
+#pragma unroll
+      for (int v = 0; v < VEC; ++v) x[v] = In::get(raw, v);
+      if (p.has_scale) {
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) x[v] = x[v] * p.scale;
+      }
+      Reg::set(data[i], x);
+    }
+  }
+  Normalizer<T> norm[VEC];
+#pragma unroll
+  for (int v = 0; v < VEC; ++v) norm[v] = g.active ? Normalizer<T>(lds_m[g.feature + v], lds_s[g.feature + v])
+                                                   : Normalizer<T>();
+  const Rsrc out = make_rsrc(static_cast<T*>(p.out) + it.start * p.d, elems * (int64_t)sizeof(T));
+#pragma unroll
+  for (int i = 0; i < RPT; ++i) {
+    if (i != 0 && wave_row0 + i * rstep >= it.rows) continue;
+    float y[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) y[v] = norm[v](Reg::get(data[i], v));
+    uint32_t w[In::kCount];
+    In::set(w, y);
+    buffer_store<In::kBytes>(out, voff + i * step, 0, w);
   }
   if (p.visits && t == 0 && it.c == 0) atomicAdd(p.visits + it.seg, 1);
   __syncthreads();
@@ -931,7 +987,7 @@ __device__ __forceinline__ void drain_and_finish(const Params& p, int64_t active
     if (claim == -1) break;
     if (claim == -2) continue;    // never written in time: the last workgroup sees it
     const int64_t slot = claim >> 32, idx = claim & 0xffffffffll;
-    if (finish_deferred<T, VEC, MASK>(p, idx, p.drain_ticks, false, lds_m, lds_s, stage) && t == 0)
+    if (finish_deferred<T, VEC, RPT, MASK, STORE_F32>(p, idx, p.drain_ticks, false, lds_m, lds_s, stage) && t == 0)
       __hip_atomic_store(p.deferred + slot, (int64_t)-1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   // A workgroup that deferred or finished a chunk took part in the drain
@@ -939,11 +995,22 @@ __device__ __forceinline__ void drain_and_finish(const Params& p, int64_t active
   // visible to the last workgroup before it counts out.
   if (!last_out(p, flag_s, active, seen)) return;
   const int64_t listed_n = (int64_t)listed();
-  for (int64_t j = 0; j < listed_n; ++j) {
-    const int64_t entry = __hip_atomic_load(p.deferred + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (entry > 0) (void)finish_deferred<T, VEC, MASK>(p, entry - 1, p.fold_ticks, true, lds_m, lds_s, stage);
+  // The list read kBlock entries per round trip (one thread each); the
+  // entries still unfinished (normally none) are then finished one by one.
+  __shared__ int64_t sweep_s[kBlock];
+  for (int64_t j0 = 0; j0 < listed_n; j0 += kBlock) {
+    __syncthreads();
+    sweep_s[t] = j0 + t < listed_n
+                     ? __hip_atomic_load(p.deferred + j0 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : 0;
+    if (j0 + t < listed_n) p.deferred[j0 + t] = 0;     // the list returns to zero
+    __syncthreads();
+    if (!block_any(sweep_s[t] > 0)) continue;
+    for (int k = 0; k < kBlock; ++k) {
+      const int64_t entry = sweep_s[k];
+      if (entry > 0) (void)finish_deferred<T, VEC, RPT, MASK, STORE_F32>(p, entry - 1, p.fold_ticks, true, lds_m, lds_s, stage);
+    }
   }
-  for (int64_t j = t; j < listed_n; j += kBlock) p.deferred[j] = 0;
   // What this call left nonzero in the arena, for the next call's
   // k_classify: the pairs of the direct chunks (bottom of the pair table)
   // and of the tree chunks (top), and the group rows.

@@ -155,3 +155,23 @@ def test_waits_end_when_workgroups_are_short(chunks):
     print(f"{chunks} chunks on 4 workgroups: {times} ms")
     assert min(times) < 0.25 * rounds * 2.0, f"waits ran to their 2 ms bound: {times} ms for {rounds} rounds"
     module.close()
+
+
+@pytest.mark.parametrize("dtype,d,longest,scale", [("bf16", 128, 300_000, 1.0), ("f32", 16, 1_500_000, 1.0),
+                                                  ("bf16", 64, 500_000, 0.5)])
+def test_segments_beyond_the_resident_grid(artifact_cache, dtype, d, longest, scale):
+    """A segment of more chunks than the device holds at once: its chunks
+    publish their statistics without waiting and are all finished by the
+    kernel's drain (re-read with the register path's row mapping and
+    arithmetic), next to segments that wait; the deferred list is swept by
+    the last workgroup a block of entries at a time."""
+    kwargs = {"scale": scale} if scale != 1.0 else {}
+    program = compile_softmax(artifact_cache, dtype, d, **kwargs)
+    capacity = int(program.metadata["part_rows"])
+    lengths = np.array([17, longest, 3 * capacity + 5, 0, 40 * capacity, 1], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = np.random.default_rng(longest).normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    for select in ("classified", "naive"):
+        actual, report = run_program(program, values, offsets, dtype=dtype, op="softmax", select=select)
+        assert report.selected == select
+        check(actual, values, offsets, op="softmax", dtype=dtype, scale=scale)
