@@ -93,18 +93,21 @@ def _grid(ds, elements, segments, seed0, count, seed_grid):
 
 
 SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5", "heldout6",
-          "heldout7", "heldout8", "heldout9")
+          "heldout7", "heldout8", "heldout9", "heldout10")
 
 
 def suite(name: str) -> list[Case]:
     """The fixed shape suites. The held-out suites share no feature width,
     size or segment count with either train suite or with each other;
-    heldout, heldout2, heldout3, heldout5, heldout6, heldout7, heldout8 and
-    heldout9 reach beyond the 256 MiB Infinity Cache (working sets up to 512,
-    384, 320, 384, 576, 352, 416 and 480 MiB). Each was frozen before the fit
-    it scores and scored once for it: ``heldout9`` was defined, pinned and
-    committed before any of it was measured, to score the model refitted on
-    the build with the two-launch register-resident softmax;
+    heldout, heldout2, heldout3, heldout5, heldout6, heldout7, heldout8,
+    heldout9 and heldout10 reach beyond the 256 MiB Infinity Cache (working
+    sets up to 512, 384, 320, 384, 576, 352, 416, 480 and 544 MiB). Each was
+    frozen before the fit it scores and scored once for it: ``heldout10`` was
+    defined, pinned and committed before any of it was measured, to score the
+    model refitted on the build whose register-resident softmax drains
+    deferred chunks at the register path's speed; ``heldout9``, likewise, for
+    the model refitted on the build with the two-launch register-resident
+    softmax;
     ``heldout8`` for the shipped model (fitted on every other suite pooled:
     their measurements on the shipped library); ``heldout7`` for the same
     model form fitted on the eight suites before it, measured on the build
@@ -151,6 +154,9 @@ def suite(name: str) -> list[Case]:
     if name == "heldout9":
         return _grid(ds=(19, 34, 60, 120, 240), elements=(15 << 18, 15 << 21, 15 << 22),
                      segments=(704, 5632, 45056), seed0=37000, count=150, seed_grid=79)
+    if name == "heldout10":
+        return _grid(ds=(21, 38, 68, 136, 248), elements=(17 << 18, 17 << 21, 17 << 22),
+                     segments=(832, 4608, 53248), seed0=41000, count=150, seed_grid=83)
     raise ValueError(f"suite must be one of {SUITES}")
 
 
