@@ -159,19 +159,19 @@ def test_evaluate_counts_within_three_percent():
 
 
 TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5", "heldout6",
-                "heldout7", "heldout8")
-HELDOUT = "heldout9"
-# The commit that froze heldout9's definition (and pinned its first keys)
+                "heldout7", "heldout8", "heldout9")
+HELDOUT = "heldout10"
+# The commit that froze heldout10's definition (and pinned its first keys)
 # before any of it was measured.
-HELDOUT_COMMIT = "ff93b6565e367dfb282bc4d6c6ad1fe9b0e2a7d6"
+HELDOUT_COMMIT = "5dbc1ad85156d4474e428a29cf405c647f3f69a5"
 
 
 def test_shipped_model_records_its_heldout_scores():
     """The committed cost model is the fit of the committed MI355X
-    measurements of every suite but heldout9, pooled (refitting reproduces
+    measurements of every suite but heldout10, pooled (refitting reproduces
     its coefficients and margins), all measured with the library whose
     sha256 it records; its choices, as run(select="auto") makes them, are
-    scored on heldout9 (its definition committed before any of it was
+    scored on heldout10 (its definition committed before any of it was
     measured, disjoint shapes, scored once) warm and cold exactly as
     recorded, and its leave-one-suite-out scores over the train suites are
     recorded as recomputed. Every measured case passed the sampled
