@@ -62,11 +62,15 @@ constexpr int kGroup = kTreeGroup;   // chunks merged per first-level group
 constexpr int kPollSleep = 64;
 
 // The work ticket counter (counters[4]) holds two counts: tickets handed out
-// (low 32 bits) and chunks deferred to the drain (high 32 bits; a deferral
-// adds 2^32 and takes its deferred-list slot from the old value). Every
-// ticket fetch so also tells a workgroup how many chunks were deferred by
-// then, and a workgroup that leaves having seen none -- the common case --
-// leaves without a further round trip. The plan keeps tickets below 2^32.
+// after the first round (low 32 bits) and chunks deferred to the drain (high
+// 32 bits; a deferral adds 2^32 and takes its deferred-list slot from the old
+// value). The first round of tickets is the workgroup index -- a thousand
+// first fetches from one address would serialise the launch (~12.5 ns each:
+// the last workgroup started 12 us late; C5's kernel 15 us faster without
+// them) -- and a fetch returning k hands out ticket gridDim.x + k. Every
+// ticket fetch also tells a workgroup how many chunks were deferred by then,
+// and a workgroup that leaves having seen none -- the common case -- leaves
+// without a further round trip. The plan keeps tickets below 2^32.
 constexpr uint64_t kTicketMask = 0xffffffffull;
 constexpr int kDeferShift = 32;
 
@@ -399,7 +403,8 @@ __device__ __forceinline__ bool poll_fold(const uint64_t* base, int64_t count, i
 }
 
 // A wait also ends, before its budget, once the segment still has chunks
-// not handed out (ticket counter <= last_ticket) and the ticket counter has
+// not handed out (ticket counter <= last_ticket, both counting the tickets
+// after the first round) and the ticket counter has
 // not moved over an interval of spin_ticks / kStallDivisor (100 us with the
 // default budget): every workgroup that could take them is then busy
 // (waiting, or another process holds the CUs), so waiting longer gains
@@ -577,9 +582,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     if (ticket < n_split + n_block) return load_item(block_items + (ticket - n_split));
     return load_item(block_items + (p.b - 1 - (ticket - n_split - n_block)));
   };
-  if (t == 0) next_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
+  if (t == 0) next_s = 0;
   __syncthreads();
-  int64_t ticket = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
+  int64_t ticket = blockIdx.x;
   Item it;
   if (ticket < total) it = item_at(ticket);
   while (ticket < total) {
@@ -673,7 +678,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     int64_t next = 0;
     Item next_it;
     if (opaque(early)) {
-      next = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
+      next = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask) + gridDim.x;
       if (next < total) next_it = item_at(next);
     }
     // 2. Column sums of exp(x - m); the rows stay as loaded. A column of
@@ -748,7 +753,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       if (!may_wait) {
         defer = true;        // more chunks than the device surely holds at once
       } else {
-        const int64_t last_ticket = ticket - it.c + parts - 1;
+        const int64_t last_ticket = ticket - it.c + parts - 1 - gridDim.x;
         const int64_t* tickets = p.counters + 4;
         const bool ready = direct ? wait_fold<kAccurate>(p.pairs + first * d, parts, p.d, p.spin_ticks, tickets,
                                                          last_ticket, lds, lds_s, stage)
@@ -800,7 +805,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
     if (!opaque(early)) {
       if (t == 0) next_s = (int64_t)taken;
       __syncthreads();
-      next = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
+      next = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask) + gridDim.x;
       if (next < total) next_it = item_at(next);
     }
     if (opaque(p.trace && ticket < p.trace_cap) && t == 0) {
@@ -834,7 +839,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) voi
       __syncthreads();
       if (t == 0) next_s = (int64_t)atomicAdd((unsigned long long*)(p.counters + 4), 1ull);
       __syncthreads();
-      ticket = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask);
+      ticket = (int64_t)((uint64_t)uniform64(next_s) & kTicketMask) + gridDim.x;
     }
   }
   // The last ticket fetch (next_s, as fetched) counted the chunks deferred
