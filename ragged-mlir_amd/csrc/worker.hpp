@@ -629,16 +629,21 @@ __global__ __launch_bounds__(kBlock) void k_worker(Params p) {
   // every ticket is a batch of segments in order: batches are alike, so
   // the hand-out atomic's round trip buys no balance.
   const bool static_tickets = direct || in_order;
+  // The first round of tickets is the workgroup index (a round of first
+  // fetches would queue on each lane's counter); a lane's fetch returning c
+  // then hands out active + c * lanes + lane.
   int64_t next = blockIdx.x;
+  bool first = true;
   for (;;) {
     int64_t ticket = next;
-    if (!static_tickets) {
+    if (!static_tickets && !first) {
       __syncthreads();
-      if (t == 0) ticket_s = (int64_t)atomicAdd(counter, 1ull) * lanes + lane_id;
+      if (t == 0) ticket_s = active + (int64_t)atomicAdd(counter, 1ull) * lanes + lane_id;
       __syncthreads();
       ticket = (int64_t)(((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)ticket_s >> 32)) << 32) |
                          __builtin_amdgcn_readfirstlane((uint32_t)(uint64_t)ticket_s));
     }
+    first = false;
     next += gridDim.x;
     if (ticket >= total) break;
     if (ticket < n_parts) {
