@@ -512,16 +512,16 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
   // extent known to be zero, before the kernel that polls them starts. A
   // workspace as allocated is all zero.
   if (p.arena_bytes > 0) {
-    const int64_t mark = p.counters[kCleanSlot];
+    // The workgroups past the segments' zero the arena alone, so that the
+    // classification's workgroups are not held up by it (they do not even
+    // read the record); without such workgroups every thread takes a share.
+    const int64_t classifying = (p.b + blockDim.x - 1) / blockDim.x;
+    const bool extra = gridDim.x > classifying;
+    const int64_t first = extra ? classifying * blockDim.x : 0;
+    const int64_t mark = !extra || (int64_t)blockIdx.x >= classifying ? p.counters[kCleanSlot] : 0;
     if (mark != 0) {
       const int64_t clean = mark == 1 ? 0 : (mark - 2 < p.arena_bytes ? mark - 2 : p.arena_bytes);
-      // The workgroups past the segments' zero the arena alone, so that the
-      // classification's workgroups are not held up by it; without such
-      // workgroups every thread takes a share.
-      const int64_t classifying = (p.b + blockDim.x - 1) / blockDim.x;
-      const bool extra = gridDim.x > classifying;
-      const int64_t first = extra ? classifying * blockDim.x : 0;
-      if (!extra || (int64_t)blockIdx.x >= classifying) {
+      {
         const int64_t threads = (int64_t)gridDim.x * blockDim.x - first;
         const int64_t tid = s - first;
         // [lo, hi) widened to 16-byte words: the bytes it adds are zero
@@ -555,7 +555,16 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
   // of the run in wave order, so a wave's (and the workgroup's) segments of
   // one class sit in consecutive positions in segment order
   // (classified-abi.md:56-66).
-  __shared__ long long run_s[4][kClassifyWaves];
+  //
+  // The register-resident softmax (p.items set) also reserves its split
+  // segments' items in the same round of atomics: the direct chunks (runs
+  // 4), the tree chunks (5) and the tree segments' group rows (6), each
+  // workgroup's total with one atomic and each segment's range at its
+  // exclusive prefix within the workgroup, in segment order. A reservation
+  // per segment after the queue's would be one more dependent round trip,
+  // and its result would also wait for the queue stores issued before it
+  // (vmcnt counts loads and stores in issue order).
+  __shared__ long long run_s[7][kClassifyWaves];
   const int wave = threadIdx.x / kWave;
   uint64_t ballots[4];
 #pragma unroll
@@ -563,16 +572,39 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
     ballots[c] = __ballot(active && cls == c);
     if (lane == 0) run_s[c][wave] = (long long)__popcll(ballots[c]);
   }
+  const bool split_items = p.items != nullptr;
+  const long long split_parts = split_items && active && cls == 2 ? (length + p.part_rows - 1) / p.part_rows : 0;
+  const bool tree = split_parts > kDirect;
+  long long split_before[3] = {0, 0, 0};   // direct parts, tree parts, group rows of the wave's lanes below
+  if (split_items && ballots[2] != 0) {
+    const long long mine3[3] = {tree ? 0 : split_parts, tree ? split_parts : 0,
+                                tree ? (split_parts + kTreeGroup - 1) / kTreeGroup : 0};
+#pragma unroll
+    for (int r = 0; r < 3; ++r) {
+      long long x = mine3[r];
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const long long y = __shfl_up(x, off, kWave);
+        if (lane >= off) x += y;
+      }
+      split_before[r] = x - mine3[r];
+      if (lane == kWave - 1) run_s[4 + r][wave] = x;
+    }
+  } else if (split_items && lane == 0) {
+    run_s[4][wave] = run_s[5][wave] = run_s[6][wave] = 0;
+  }
   __syncthreads();
-  if (threadIdx.x < 4) {
+  if (threadIdx.x < (split_items ? 7 : 4)) {
     const int c = threadIdx.x;
     long long total = 0;
     for (int w = 0; w < waves; ++w) total += run_s[c][w];
     // Run 3 is counted in counters[8]. A register-resident softmax
     // (block_items set) counts run 0 in counters[7]: k_softmax_deferred
     // takes the wave class, and k_softmax_fused, which reads counters[0],
-    // sees none.
-    const int slot = c == 3 ? 8 : c == 0 && p.block_items ? 7 : c;
+    // sees none. Its split reservations: direct chunks in counters[3], tree
+    // chunks (from the top of the item array) in counters[6], group rows in
+    // counters[kGroupRowSlot].
+    const int slot = c == 3 ? 8 : c == 0 && p.block_items ? 7 : c == 4 ? 3 : c == 5 ? 6 : c == 6 ? kGroupRowSlot : c;
     long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + slot), (unsigned long long)total) : 0;
     for (int w = 0; w < waves; ++w) {
       const long long count = run_s[c][w];
@@ -601,19 +633,30 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
     // first, while every workgroup of the grid is still free to hold one.
     long long first = 0, parts = 0, gbase = 0;
     bool fits = true;
-    if (mine && pos < p.b_split) {
-      parts = (length + p.part_rows - 1) / p.part_rows;
-      if (p.items && parts > kDirect) {
-        const long long above = (long long)atomicAdd((unsigned long long*)(p.counters + 6), (unsigned long long)parts);
+    if (mine && split_items) {
+      // Reserved before the queue position was known: a segment past b_split
+      // (clamped invalid offsets only) still owns its items, written empty.
+      const bool owned = pos < p.b_split;
+      parts = split_parts;
+      if (tree) {
+        const long long above = run_s[5][wave] + split_before[1];
         first = (long long)p.items_cap - above - parts;
         // The segment's rows of final_pairs, one per group of kTreeGroup.
         const long long groups = (parts + kTreeGroup - 1) / kTreeGroup;
-        gbase = (long long)atomicAdd((unsigned long long*)(p.counters + kGroupRowSlot), (unsigned long long)groups);
-        fits = first >= 0 && gbase + groups <= tree_group_rows(p.items_cap);
+        gbase = run_s[6][wave] + split_before[2];
+        fits = owned && first >= 0 && gbase + groups <= tree_group_rows(p.items_cap);
       } else {
-        first = (long long)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
-        fits = first + parts <= p.items_cap;
+        first = run_s[4][wave] + split_before[0];
+        fits = owned && first + parts <= p.items_cap;
       }
+      if (owned && p.part_begin) p.part_begin[pos] = first;
+      if (owned && p.seg_arrive) p.seg_arrive[pos] = 0;
+    } else if (mine && pos < p.b_split) {
+      // Streaming worker: a reserved item must name a queued segment, so the
+      // reservation waits for the queue position.
+      parts = (length + p.part_rows - 1) / p.part_rows;
+      first = (long long)atomicAdd((unsigned long long*)(p.counters + 3), (unsigned long long)parts);
+      fits = first + parts <= p.items_cap;
       if (p.part_begin) p.part_begin[pos] = first;
       // The segment's part arrivals start at zero (streaming worker; the
       // register-resident softmax's counters are in its arena).
