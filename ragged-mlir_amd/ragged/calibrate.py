@@ -93,16 +93,20 @@ def _grid(ds, elements, segments, seed0, count, seed_grid):
 
 
 SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5", "heldout6",
-          "heldout7", "heldout8", "heldout9", "heldout10")
+          "heldout7", "heldout8", "heldout9", "heldout10", "heldout11")
 
 
 def suite(name: str) -> list[Case]:
     """The fixed shape suites. The held-out suites share no feature width,
     size or segment count with either train suite or with each other;
     heldout, heldout2, heldout3, heldout5, heldout6, heldout7, heldout8,
-    heldout9 and heldout10 reach beyond the 256 MiB Infinity Cache (working
-    sets up to 512, 384, 320, 384, 576, 352, 416, 480 and 544 MiB). Each was
-    frozen before the fit it scores and scored once for it: ``heldout10`` was
+    heldout9, heldout10 and heldout11 reach beyond the 256 MiB Infinity Cache
+    (working sets up to 512, 384, 320, 384, 576, 352, 416, 480, 544 and 608
+    MiB). Each was frozen before the fit it scores and scored once for it:
+    ``heldout11`` was defined, pinned and committed before any of it was
+    measured, to score the boosted model form (version 7) fitted on every
+    earlier suite measured on the build whose classification reserves split
+    items in one round of atomics; ``heldout10`` was
     defined, pinned and committed before any of it was measured, to score the
     model refitted on the build whose register-resident softmax drains
     deferred chunks at the register path's speed; ``heldout9``, likewise, for
@@ -157,6 +161,9 @@ def suite(name: str) -> list[Case]:
     if name == "heldout10":
         return _grid(ds=(21, 38, 68, 136, 248), elements=(17 << 18, 17 << 21, 17 << 22),
                      segments=(832, 4608, 53248), seed0=41000, count=150, seed_grid=83)
+    if name == "heldout11":
+        return _grid(ds=(23, 42, 76, 152, 232), elements=(19 << 18, 19 << 21, 19 << 22),
+                     segments=(960, 3584, 61440), seed0=45000, count=150, seed_grid=89)
     raise ValueError(f"suite must be one of {SUITES}")
 
 
