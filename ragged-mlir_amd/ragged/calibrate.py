@@ -17,13 +17,17 @@ Restates the protocol of the reference's ``bench/calibrate.py`` (:89-226,
   tolerances). It appends one JSON line per case, with the library's
   sha256, and skips cases already in the file, so an interrupted run
   resumes.
-* ``fit`` solves, per operation family and schedule, a nonnegative least
-  squares problem on relative error (each row divided by its measured
-  time) over all terms, on the cases where ``run(select="auto")`` consults
-  the model (not those whose max_len sends them to the short-segment
-  schedule), reports its leave-one-shape-out error, and then picks per
-  family the decision margin that maximises the share of the family's
-  training cases within 3% of the faster schedule.
+* ``fit`` fits, per operation family and schedule, on the cases where
+  ``run(select="auto")`` consults the model (not those whose max_len sends
+  them to the short-segment schedule): by default (model version 7) a
+  boosted ensemble of depth-4 regression trees on log(µs) over the host
+  statistics (``BOOST``: squared loss, 150 trees, learning rate 0.1, 80%
+  subsamples drawn from a fixed seed, so a refit reproduces it); with
+  ``form="linear"`` (version 6) a nonnegative least squares problem on
+  relative error (each row divided by its measured time) over the eleven
+  terms, with its leave-one-shape-out error. It then picks per family the
+  decision margin that maximises the share of the family's training cases
+  within 3% of the faster schedule.
 * ``evaluate`` reports, for a suite's measurements, how many of the
   schedules ``run(select="auto")`` takes fall within 3% of the faster
   measured schedule, warm and (where measured) cold: the short-segment
@@ -54,7 +58,7 @@ import time
 import numpy as np
 
 from .optimizations import Optimizations
-from .selection import FAMILIES, SCHEDULES, TERMS, VERSION, CostModel, family, features
+from .selection import FAMILIES, SCHEDULES, TERMS, VERSION, CostModel, Ensemble, family, features, host_features
 from .workloads import make_lengths, offsets_from_lengths
 
 WITHIN = 0.03     # a choice is good when its measured time is within 3% of the faster schedule
@@ -425,58 +429,156 @@ def evaluate(model: CostModel, records: list[dict], device_l2: bool = False, col
             "misses": misses}
 
 
-def fit(records: list[dict]) -> dict:
-    """The cost model file for ``records`` (train measurements)."""
-    coefficients, errors = {}, {}
+# The version-7 ensembles: squared loss on log(µs), depth-4 trees, fixed
+# subsample seed (chosen by leave-one-suite-out over the suites measured
+# before heldout11; the held-out suite took no part).
+BOOST = {"max_depth": 4, "n_estimators": 150, "learning_rate": 0.1, "subsample": 0.8, "random_state": 0}
+
+
+def _host_row(record: dict) -> list[float]:
+    element = 2 if record["dtype"] == "bf16" else 4
+    return list(host_features(record["n"], record["b"], record["d"], record["max_len"], element, record["op"],
+                              flat=_flat(record)))
+
+
+def _complete_tree(tree, depth: int) -> tuple[list[int], list[float], list[float]]:
+    """A fitted sklearn regression tree as a complete tree of ``depth``
+    (heap order): a leaf above the last level becomes internal nodes that
+    always go left (threshold 1e300) over copies of its value."""
+    t = tree.tree_
+    inner = 2**depth - 1
+    feats, thresholds, leaves = [0] * inner, [1e300] * inner, [0.0] * (inner + 1)
+
+    def place(node: int, pos: int, level: int) -> None:
+        if level == depth:
+            leaves[pos - inner] = float(t.value[node].reshape(-1)[0])
+            return
+        if t.children_left[node] == -1:
+            place(node, 2 * pos + 1, level + 1)
+            place(node, 2 * pos + 2, level + 1)
+            return
+        feats[pos], thresholds[pos] = int(t.feature[node]), float(t.threshold[node])
+        place(int(t.children_left[node]), 2 * pos + 1, level + 1)
+        place(int(t.children_right[node]), 2 * pos + 2, level + 1)
+
+    place(0, 0, 0)
+    return feats, thresholds, leaves
+
+
+def fit_ensemble(records: list[dict], schedule: str) -> Ensemble:
+    """The version-7 ensemble for one family and schedule: log(µs) of
+    ``records`` over their host statistics."""
+    try:
+        from sklearn.ensemble import GradientBoostingRegressor
+    except ImportError as exc:   # the runtime needs no sklearn; fitting does
+        raise RuntimeError("fitting a version-7 cost model needs scikit-learn") from exc
+    x = np.array([_host_row(r) for r in records])
+    y = np.log(np.array([r["us"][schedule] for r in records], dtype=np.float64))
+    model = GradientBoostingRegressor(**BOOST).fit(x, y)
+    depth = BOOST["max_depth"]
+    trees = [_complete_tree(estimator[0], depth) for estimator in model.estimators_]
+    rate = BOOST["learning_rate"]
+    base = float(np.asarray(model.init_.predict(x[:1])).reshape(-1)[0])
+    ensemble = Ensemble.from_dict({"base": base, "depth": depth, "features": [t[0] for t in trees],
+                                   "thresholds": [t[1] for t in trees],
+                                   "leaves": [[rate * v for v in t[2]] for t in trees]})
+    # The stored trees reproduce the fitted model.
+    assert np.allclose(ensemble.log_us(x), model.predict(x), rtol=0, atol=1e-9)
+    return ensemble
+
+
+def _best_margin(records: list[dict], predicted: list[tuple[float, float] | None]) -> float:
+    """The smallest margin in [0, 0.5) steps of 0.01 that maximises the
+    share of ``records`` whose choice is within 3% of the faster schedule
+    (``predicted``: (classified, naive) µs, or None where the short-segment
+    rule decides)."""
+    best_margin, best_good = 0.0, -1
+    for margin in np.arange(0.0, 0.5, 0.01):
+        margin = float(round(margin, 2))
+        good = 0
+        for record, pair in zip(records, predicted):
+            chosen = "classified" if pair is None or pair[0] < pair[1] * (1 - margin) else "naive"
+            good += record["us"][chosen] <= min(record["us"].values()) * (1 + WITHIN)
+        if good > best_good:
+            best_margin, best_good = margin, good
+    return best_margin
+
+
+def fit(records: list[dict], form: str = "boosted") -> dict:
+    """The cost model file for ``records`` (train measurements): version 7
+    (``form="boosted"``) or version 6 (``"linear"``)."""
+    if form not in ("boosted", "linear"):
+        raise ValueError("form must be 'boosted' or 'linear'")
     modelled = [r for r in records if not short_segments(r)]
+    data = {"version": 7 if form == "boosted" else 6, "margins": {name: 0.0 for name in FAMILIES},
+            "l2_mib": 32.0, "mall_mib": 256.0, "calibration": {}}
+    errors = {}
     for name in FAMILIES:
         subset = [r for r in modelled if _family(r) == name]
         if len(subset) < TERMS:
             raise ValueError(f"too few {name} measurements to fit ({len(subset)})")
-        coefficients[name], errors[name] = {}, {}
-        for schedule in SCHEDULES:
-            coef, error = fit_family(subset, schedule)
-            coefficients[name][schedule] = [round(float(c), 6) for c in coef]
-            errors[name][schedule] = round(error, 4)
-    data = {"version": VERSION, "coefficients": coefficients, "margins": {name: 0.0 for name in FAMILIES},
-            "l2_mib": 32.0, "mall_mib": 256.0, "calibration": {}}
+        if form == "boosted":
+            data.setdefault("ensembles", {})[name] = {s: fit_ensemble(subset, s).to_dict() for s in SCHEDULES}
+        else:
+            data.setdefault("coefficients", {})[name], errors[name] = {}, {}
+            for schedule in SCHEDULES:
+                coef, error = fit_family(subset, schedule)
+                data["coefficients"][name][schedule] = [round(float(c), 6) for c in coef]
+                errors[name][schedule] = round(error, 4)
     # Margins: a family classifies only when predicted faster by its margin;
     # each is the one that maximises within-3% choices on the family's
     # training cases (the smallest such).
+    model = CostModel.from_dict(data)
     for name in FAMILIES:
         subset = [r for r in records if _family(r) == name]
-        best_margin, best_share = 0.0, -1.0
-        for margin in np.arange(0.0, 0.5, 0.01):
-            data["margins"][name] = float(round(margin, 2))
-            share = evaluate(CostModel.from_dict(data), subset)["share"]
-            if share > best_share + 1e-12:
-                best_margin, best_share = data["margins"][name], share
-        data["margins"][name] = best_margin
+        predicted = []
+        for record in subset:
+            if short_segments(record):
+                predicted.append(None)
+                continue
+            element = 2 if record["dtype"] == "bf16" else 4
+            args = (record["op"], record["n"], record["b"], record["d"], record["max_len"], element)
+            kwargs = {"fused": bool(record.get("fused", False)), "flat": _flat(record)}
+            predicted.append((model.predict("classified", *args, **kwargs), model.predict("naive", *args, **kwargs)))
+        data["margins"][name] = _best_margin(subset, predicted)
     best_share = evaluate(CostModel.from_dict(data), records)["share"]
     libraries = sorted({r["library_sha256"] for r in records if r.get("library_sha256")})
-    data["calibration"] = {
+    calibration = {
         "status": "fitted on MI355X measurements (python -m ragged.calibrate fit)",
-        "library_sha256": libraries[0] if len(libraries) == 1 else libraries,
-        "terms": "t_us = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + c7*X_mall + c8*W*A "
-                 "+ c9*W*U + c10*S*U",
-        "method": "per family and schedule: NNLS on relative error over all terms, on the cases the runtime "
-                  "models (leave-one-shape-out error reported); per family the margin maximising the family's "
-                  "training choices within 3% of the faster schedule; choices scored as run(select='auto') "
-                  "makes them (short-segment rule first)",
-        "train_cases": len(records), "leave_one_shape_out_error": errors, "train_within_3pct": best_share}
+        "library_sha256": libraries[0] if len(libraries) == 1 else libraries}
+    if form == "boosted":
+        calibration["terms"] = ("log(t_us) = base + sum of tree leaves over host_features: log2(moved MiB / L2 MiB), "
+                                "log2 B, log2 longest-segment MiB, log2(L / (N/B)), log2 row bytes, flat, "
+                                "16/access bytes - 1, 1/lane utilisation - 1, log2 mean-segment MiB")
+        calibration["method"] = (f"per family and schedule: gradient-boosted regression trees on log(us) ({BOOST}), "
+                                 "on the cases the runtime models; per family the margin maximising the family's "
+                                 "training choices within 3% of the faster schedule; choices scored as "
+                                 "run(select='auto') makes them (short-segment rule first)")
+    else:
+        calibration["terms"] = ("t_us = c0 + c1*W + c2*S + c3*B/1000 + c4*F*B/1000 + c5*R*B/1000 + c6*X_l2 + "
+                                "c7*X_mall + c8*W*A + c9*W*U + c10*S*U")
+        calibration["method"] = ("per family and schedule: NNLS on relative error over all terms, on the cases the "
+                                 "runtime models (leave-one-shape-out error reported); per family the margin "
+                                 "maximising the family's training choices within 3% of the faster schedule; choices "
+                                 "scored as run(select='auto') makes them (short-segment rule first)")
+        calibration["leave_one_shape_out_error"] = errors
+    calibration["train_cases"] = len(records)
+    calibration["train_within_3pct"] = best_share
+    data["calibration"] = calibration
     if all("us_cold" in r for r in records):
         data["calibration"]["train_within_3pct_cold"] = evaluate(CostModel.from_dict(data), records, cold=True)["share"]
     return data
 
 
-def leave_one_suite_out(files: dict[str, list[dict]]) -> dict:
+def leave_one_suite_out(files: dict[str, list[dict]], form: str = "boosted") -> dict:
     """Each measurement file held out in turn: the model form fitted on the
     others pooled, scored on it warm and cold (the share of choices within
     3% of the faster schedule, as run(select="auto") makes them), and the
     means over the files."""
     report = {}
     for held in files:
-        model = CostModel.from_dict(fit([r for name, records in files.items() if name != held for r in records]))
+        model = CostModel.from_dict(fit([r for name, records in files.items() if name != held for r in records],
+                                        form))
         report[held] = {"cases": len(files[held]), "within_3pct": evaluate(model, files[held])["share"],
                         "within_3pct_cold": evaluate(model, files[held], cold=True)["share"]}
     report["mean_within_3pct"] = round(float(np.mean([r["within_3pct"] for r in report.values()])), 4)
@@ -501,6 +603,16 @@ def transfer(train: list[dict], heldout: list[dict], shipped: CostModel) -> tupl
     return data, report
 
 
+def dump_model(data: dict) -> str:
+    """A model file's text: indented, but each version-7 ensemble on one line."""
+    text = json.dumps({k: v for k, v in data.items() if k != "ensembles"}, indent=2)
+    if "ensembles" in data:
+        text = text[:-2] + ',\n  "ensembles": {\n' + ",\n".join(
+            f"    {json.dumps(name)}: {json.dumps(value, separators=(',', ':'))}"
+            for name, value in data["ensembles"].items()) + "\n  }\n}"
+    return text + "\n"
+
+
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = parser.add_subparsers(dest="command", required=True)
@@ -517,6 +629,8 @@ def main(argv=None) -> int:
     f.add_argument("--loso", action="store_true",
                    help="also record the leave-one-suite-out scores over the train files")
     f.add_argument("--heldout-commit", help="commit that froze the held-out suite's definition (recorded)")
+    f.add_argument("--form", choices=("boosted", "linear"), default="boosted",
+                   help="model version 7 (boosted trees, default) or 6 (linear terms)")
     e = sub.add_parser("evaluate")
     e.add_argument("results", type=Path)
     e.add_argument("--model", type=Path)
@@ -535,7 +649,7 @@ def main(argv=None) -> int:
         return 0
     if args.command == "fit":
         records = [record for path in args.results for record in load(path)]
-        data = fit(records)
+        data = fit(records, args.form)
         data["calibration"]["train_file"] = " + ".join(path.name for path in args.results)
         data["calibration"]["device"] = ("gfx950 (the library's only target); L2 MiB measured: "
                                          f"{sorted({r['l2_mib'] for r in records if r.get('l2_mib')})}")
@@ -554,21 +668,21 @@ def main(argv=None) -> int:
                 data["calibration"]["heldout_definition_commit"] = args.heldout_commit
         if args.loso:
             data["calibration"]["leave_one_suite_out"] = leave_one_suite_out(
-                {path.stem: load(path) for path in args.results})
+                {path.stem: load(path) for path in args.results}, args.form)
         for path in args.check:
             records = load(path)
             entry = {"cases": len(records), "within_3pct": evaluate(CostModel.from_dict(data), records)["share"]}
             if all("us_cold" in r for r in records):
                 entry["within_3pct_cold"] = evaluate(CostModel.from_dict(data), records, cold=True)["share"]
             data["calibration"].setdefault("checks", {})[path.name] = entry
-        args.out.write_text(json.dumps(data, indent=2) + "\n")
+        args.out.write_text(dump_model(data))
         print(json.dumps(data["calibration"], indent=2))
         return 0
     if args.command == "transfer":
         shipped = CostModel.load(args.model) if args.model else CostModel.load()
         data, report = transfer(load(args.train), load(args.heldout), shipped)
         data["calibration"]["train_file"] = args.train.name
-        args.out.write_text(json.dumps(data, indent=2) + "\n")
+        args.out.write_text(dump_model(data))
         print(json.dumps(report, indent=2))
         return 0
     model = CostModel.load(args.model) if args.model else CostModel.load()

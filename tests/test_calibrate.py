@@ -134,7 +134,7 @@ def test_evaluate_cold_uses_cold_timings():
 
 def test_fit_recovers_known_coefficients():
     records = synthetic_records(calibrate.suite("train")[::3], TRUTH)
-    data = calibrate.fit(records)
+    data = calibrate.fit(records, "linear")
     model = CostModel.from_dict(data)
     for record in records[:20]:
         for schedule in ("classified", "naive"):
@@ -163,19 +163,19 @@ def test_evaluate_counts_within_three_percent():
 
 
 TRAIN_SUITES = ("train", "train_dense", "heldout", "heldout2", "heldout3", "heldout4", "heldout5", "heldout6",
-                "heldout7", "heldout8", "heldout9")
-HELDOUT = "heldout10"
-# The commit that froze heldout10's definition (and pinned its first keys)
+                "heldout7", "heldout8", "heldout9", "heldout10")
+HELDOUT = "heldout11"
+# The commit that froze heldout11's definition (and pinned its first keys)
 # before any of it was measured.
-HELDOUT_COMMIT = "5dbc1ad85156d4474e428a29cf405c647f3f69a5"
+HELDOUT_COMMIT = "dc2241397ed0052ea9de74c56e5ce5439ecb535f"
 
 
 def test_shipped_model_records_its_heldout_scores():
-    """The committed cost model is the fit of the committed MI355X
-    measurements of every suite but heldout10, pooled (refitting reproduces
-    its coefficients and margins), all measured with the library whose
-    sha256 it records; its choices, as run(select="auto") makes them, are
-    scored on heldout10 (its definition committed before any of it was
+    """The committed cost model (version 7) is the fit of the committed
+    MI355X measurements of every suite but heldout11, pooled (refitting
+    reproduces its ensembles and margins), all measured with the library
+    whose sha256 it records; its choices, as run(select="auto") makes them,
+    are scored on heldout11 (its definition committed before any of it was
     measured, disjoint shapes, scored once) warm and cold exactly as
     recorded, and its leave-one-suite-out scores over the train suites are
     recorded as recomputed. Every measured case passed the sampled
@@ -197,10 +197,10 @@ def test_shipped_model_records_its_heldout_scores():
     assert model.calibration["train_file"] == " + ".join(f"{name}.jsonl" for name in TRAIN_SUITES)
     assert model.calibration["heldout_within_3pct"] == warm["share"]
     assert model.calibration["heldout_within_3pct_cold"] == cold["share"]
+    assert model.version == 7
     refit = calibrate.fit([r for name in TRAIN_SUITES for r in files[name]])
-    for fam, schedules in refit["coefficients"].items():
-        for schedule, coefficients in schedules.items():
-            assert coefficients == pytest.approx(list(model.coefficients[fam][schedule]), rel=1e-4, abs=1e-6)
+    shipped = json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())
+    assert json.loads(calibrate.dump_model(refit))["ensembles"] == shipped["ensembles"]
     assert refit["margins"] == model.margins
     loso = calibrate.leave_one_suite_out({name: files[name] for name in TRAIN_SUITES})
     assert loso == model.calibration["leave_one_suite_out"]
@@ -216,8 +216,8 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     heldout = calibrate.load(directory / f"{HELDOUT}.jsonl")
     shipped = CostModel.load()
     data, report = calibrate.transfer(train, heldout, shipped)
-    assert data["coefficients"] == json.loads(Path(calibrate.__file__).with_name("cost_model.json").read_text())[
-        "coefficients"]
+    assert json.loads(calibrate.dump_model(data))["ensembles"] == json.loads(
+        Path(calibrate.__file__).with_name("cost_model.json").read_text())["ensembles"]
     assert data["margins"] == shipped.margins
     assert report["heldout_cases"] == 150
     recorded = round(shipped.calibration["heldout_within_3pct"] * 150)
@@ -226,7 +226,7 @@ def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp
     pooled = tmp_path / "train_pooled.jsonl"
     pooled.write_text("".join(json.dumps(record) + "\n" for record in train))
     assert calibrate.main(["transfer", str(pooled), str(directory / f"{HELDOUT}.jsonl"), "--out", str(out)]) == 0
-    assert json.loads(out.read_text())["coefficients"] == data["coefficients"]
+    assert json.loads(out.read_text())["ensembles"] == json.loads(calibrate.dump_model(data))["ensembles"]
 
 
 def test_evaluate_scores_the_short_segment_rule_before_the_model():
@@ -270,3 +270,117 @@ def test_transfer_gives_the_device_l2_to_the_shipped_model():
     calibrate.evaluate(spy, [{**record, "l2_mib": 8.0}])
     assert seen == [None, 8.0, None]
     assert shipped.l2_mib == 32.0
+
+
+def test_leaf_table_follows_the_decisions():
+    """Depth 4, heap order, bit i set = node i goes right: no bits is the
+    leftmost leaf, all bits the rightmost; root right, then left, left, left
+    is nodes 0 -> 2 -> 5 -> 11 -> 23, leaf 8. Bits off the path do not matter."""
+    from ragged.selection import _leaf_table
+    table = _leaf_table(4)
+    assert len(table) == 1 << 15
+    assert table[0] == 0 and table[(1 << 15) - 1] == 15
+    assert table[1] == 8
+    assert table[1 | (1 << 1) | (1 << 3)] == 8          # nodes 1 and 3 are not on that path
+    assert table[1 | (1 << 2)] == 12                   # 0 -> 2 -> 6 -> 13 -> 27: leaf 12
+    for depth in (1, 2, 3):
+        t = _leaf_table(depth)
+        assert sorted(set(t.tolist())) == list(range(2**depth))
+
+
+def _hand_ensemble(base=1.0):
+    """One depth-2 tree: root splits statistic 3 at 0.5, its children
+    statistic 0 at -1 (left) and statistic 8 at 2 (right)."""
+    from ragged.selection import Ensemble
+    return Ensemble.from_dict({"base": base, "depth": 2, "features": [[3, 0, 8]],
+                               "thresholds": [[0.5, -1.0, 2.0]], "leaves": [[0.1, 0.2, 0.3, 0.4]]})
+
+
+def test_ensemble_prediction_on_a_hand_built_tree():
+    e = _hand_ensemble()
+    x = [0.0] * 9
+    assert e.log_us(x) == pytest.approx(1.2)            # 3 <= 0.5: left; 0 > -1: right -> leaf 1
+    x[0] = -2.0
+    assert e.log_us(x) == pytest.approx(1.1)            # leaf 0
+    x[3], x[8] = 1.0, 5.0
+    assert e.log_us(x) == pytest.approx(1.4)            # right, right -> leaf 3
+    x[8] = 2.0
+    assert e.log_us(x) == pytest.approx(1.3)            # equal to the threshold goes left
+    from ragged.selection import Ensemble
+    assert Ensemble.pair_log_us(e, _hand_ensemble(2.0), x) == pytest.approx((1.3, 2.3))
+
+
+def test_paired_and_single_predictions_agree():
+    rng = np.random.default_rng(3)
+    from ragged.selection import Ensemble
+    def random_ensemble(depth, trees):
+        inner = 2**depth - 1
+        return Ensemble.from_dict({"base": float(rng.normal()), "depth": depth,
+                                   "features": rng.integers(0, 9, (trees, inner)).tolist(),
+                                   "thresholds": rng.normal(size=(trees, inner)).tolist(),
+                                   "leaves": rng.normal(size=(trees, 2**depth)).tolist()})
+    for depth in (3, 4, 5):
+        a, b = random_ensemble(depth, 20), random_ensemble(depth, 30)
+        for _ in range(50):
+            x = rng.normal(size=9)
+            assert Ensemble.pair_log_us(a, b, x) == pytest.approx((a.log_us(x), b.log_us(x)), abs=1e-12)
+
+
+def test_boosted_fit_recovers_a_step():
+    """log(µs) that steps with the skew statistic (L over the mean length)
+    is recovered by the version-7 fit on both sides of the step."""
+    from ragged.selection import host_features
+    records = synthetic_records(calibrate.suite("train")[::2], TRUTH)
+    element = {"f32": 4, "bf16": 2}
+    for r in records:
+        x = host_features(r["n"], r["b"], r["d"], r["max_len"], element[r["dtype"]], r["op"],
+                          flat=r["mapping"] == "flat")
+        r["us"] = {"classified": 40.0 if x[3] > 3 else 20.0, "naive": 30.0}
+    data = calibrate.fit(records)
+    model = CostModel.from_dict(json.loads(calibrate.dump_model(data)))
+    assert model.version == 7
+    for r in records[:40]:
+        predicted = model.predict("classified", r["op"], r["n"], r["b"], r["d"], r["max_len"], element[r["dtype"]],
+                                  fused=r["fused"], flat=r["mapping"] == "flat")
+        assert predicted == pytest.approx(r["us"]["classified"], rel=0.02)
+    assert calibrate.evaluate(model, records)["share"] == 1.0
+
+
+def test_malformed_version_7_files_are_rejected():
+    from ragged.errors import CacheMismatch
+    good = _hand_ensemble().to_dict()
+    def model(ensemble):
+        return {"version": 7, "margins": NO_MARGINS, "l2_mib": 32.0, "mall_mib": 256.0,
+                "ensembles": {f: {"classified": ensemble, "naive": good} for f in NO_MARGINS}}
+    CostModel.from_dict(model(good))
+    for bad in ({**good, "depth": 3}, {**good, "features": [[3, 0, 9]]}, {**good, "leaves": [[0.1, 0.2, 0.3]]},
+                {**good, "thresholds": [[0.5, float("nan"), 2.0]]}, {k: v for k, v in good.items() if k != "base"}):
+        with pytest.raises(CacheMismatch):
+            CostModel.from_dict(model(bad))
+    with pytest.raises(CacheMismatch):
+        CostModel.from_dict({**model(good), "version": 8})
+
+
+def test_each_model_predicts_with_its_own_trees():
+    """Models created and dropped one after another (as leave-one-suite-out
+    does) each choose by their own ensembles: a cache of flattened trees
+    keyed by object identity once served a later model a dropped model's
+    trees."""
+    import gc
+    import math
+    rng = np.random.default_rng(11)
+    from ragged.selection import host_features
+    for _ in range(30):
+        def ensemble():
+            return {"base": float(rng.normal()), "depth": 4, "features": rng.integers(0, 9, (5, 15)).tolist(),
+                    "thresholds": rng.normal(size=(5, 15)).tolist(), "leaves": rng.normal(size=(5, 16)).tolist()}
+        model = CostModel.from_dict({"version": 7, "margins": NO_MARGINS, "l2_mib": 32.0, "mall_mib": 256.0,
+                                     "ensembles": {f: {"classified": ensemble(), "naive": ensemble()}
+                                                   for f in NO_MARGINS}})
+        x = host_features(1 << 20, 4096, 32, 5000, 4, "sum")
+        _, info = model.choose("sum", 1 << 20, 4096, 32, 5000, 4)
+        for schedule in ("classified", "naive"):
+            expected = math.exp(model.ensembles["reduce"][schedule].log_us(x))
+            assert info["predicted_us"][schedule] == pytest.approx(expected, rel=1e-3, abs=0.01)
+        del model
+        gc.collect()

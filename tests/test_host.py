@@ -184,6 +184,22 @@ def test_cost_model_features_known_answer():
             assert access_bytes(d, element) == (16 if mapping == "flat" else vec * element), (d, dtype)
 
 
+
+def test_host_features_known_answers():
+    """The version-7 statistics: 2^20 rows of 4 f32 (16 B) in 1024 segments,
+    longest 2^14 rows: (16 MiB + 1024 result rows) over the 32 MiB L2, 2^10
+    segments, a 0.25 MiB longest segment 16x the mean, 16-byte rows and
+    accesses on one lane, a 1/64 MiB mean segment; D=80 f32 idles 3/8 of
+    its 32 lanes (1/0.625 - 1)."""
+    import math
+    from ragged.selection import host_features
+    x = host_features(2**20, 1024, 4, 2**14, 4, "sum")
+    assert x == pytest.approx((math.log2(16.015625 / 32), 10, -2, 4, 4, 0, 0, 0, -6))
+    assert host_features(2**20, 1024, 4, 2**14, 4, "softmax")[0] == pytest.approx(0.0)
+    assert host_features(2**20, 1024, 4, 2**14, 4, "sum", l2_mib=8.0)[0] == pytest.approx(math.log2(16.015625 / 8))
+    assert host_features(1 << 20, 4096, 80, 1000, 4, "sum")[7] == pytest.approx(0.6)
+    assert host_features(1 << 20, 4096, 2, 1000, 4, "sum", flat=True)[5:8] == (1.0, 0.0, 0.0)
+
 def test_product_fails_loudly_without_the_library(monkeypatch, tmp_path):
     monkeypatch.setattr(native, "LIBRARY_PATH", tmp_path / "missing.so")
     with pytest.raises(RuntimeUnavailable, match="missing"):
