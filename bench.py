@@ -429,9 +429,14 @@ def measured_traffic(workload: str, role: str | None):
     """HBM bytes per launch of ``role``'s kernel from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of this workload, if it was measured with
     the library that is loaded now (None otherwise)."""
-    path = ROOT / "profiles" / f"{role}_{workload}_traffic.json"
-    if not role or not path.exists():
+    if not role:
         return None
+    # Summaries are named for the kernel role, the workload and its shape:
+    # profiles/<role>_<workload>_<shape>_traffic.json.
+    paths = sorted((ROOT / "profiles").glob(f"{role}_{workload}_*traffic.json"))
+    if len(paths) != 1:
+        return None
+    path = paths[0]
     from ragged import native
     data = json.loads(path.read_text())
     if data.get("library_sha256") != native.library_sha256():

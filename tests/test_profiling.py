@@ -178,3 +178,37 @@ def test_call_passes_known_answers(tmp_path, capsys):
     out = capsys.readouterr().out
     assert "| 1 | 2 | 490.0 | 11.00 | 0.00 | 479.00 (479.0-479.0) | 0.00 |" in out
     assert "| 2 | 2 | 481.0 | 10.00 | 6.00 | 460.00 (460.0-460.0) | 10.00 |" in out
+
+
+def _bench_module():
+    import importlib.util
+    import sys
+    root = Path(__file__).resolve().parents[1]
+    spec = importlib.util.spec_from_file_location("bench_under_test", root / "bench.py")
+    module = importlib.util.module_from_spec(spec)
+    argv = sys.argv
+    try:
+        sys.argv = ["bench.py"]
+        spec.loader.exec_module(module)
+    finally:
+        sys.argv = argv
+    return module
+
+
+def test_bench_finds_the_committed_traffic_summary(monkeypatch):
+    """bench.py's roofline.traffic comes from the committed rocprofv3 summary
+    of the dominant kernel (profiles/<role>_<workload>_<shape>_traffic.json)
+    when it was measured with the library the process loads, and is null
+    otherwise."""
+    from ragged import native
+    bench = _bench_module()
+    root = Path(__file__).resolve().parents[1]
+    summary = json.loads((root / "profiles" / "fused_c5_softmax_bf16_d128_longtail_traffic.json").read_text())
+    monkeypatch.setattr(native, "library_sha256", lambda: summary["library_sha256"])
+    found = bench.measured_traffic("c5", "fused")
+    assert found == {"bytes": int(round(summary["bytes"])),
+                     "source": "profiles/fused_c5_softmax_bf16_d128_longtail_traffic.json"}
+    assert 1.0 < found["bytes"] / summary["algorithmic_bytes"] < 1.1
+    monkeypatch.setattr(native, "library_sha256", lambda: "0" * 64)
+    assert bench.measured_traffic("c5", "fused") is None
+    assert bench.measured_traffic("c5", None) is None
