@@ -212,3 +212,11 @@ def test_bench_finds_the_committed_traffic_summary(monkeypatch):
     monkeypatch.setattr(native, "library_sha256", lambda: "0" * 64)
     assert bench.measured_traffic("c5", "fused") is None
     assert bench.measured_traffic("c5", None) is None
+
+
+def test_bench_refuses_more_than_one_gpu(capsys):
+    """One GPU only: --gpus N>1 exits with status 2 and says so, before
+    touching a device."""
+    bench = _bench_module()
+    assert bench.main(["--gpus", "2"]) == 2
+    assert "one GPU only" in capsys.readouterr().err
