@@ -37,6 +37,27 @@ _device_l2_mib: dict[int, float | None] = {}
 _current_streams: dict[tuple, Any] = {}
 I64_MAX = 2**63 - 1
 
+# The register-resident softmax holds a segment's chunks only while the
+# device can hold them all: segments of more chunks than 7/8 of its resident
+# workgroups (the library's rule, rg_plan_create's wait_parts) defer every
+# chunk to the kernel's drain, which re-reads them about 3-4x slower per chunk
+# than the streaming worker's split schedule streams them. A call whose
+# deferred rows are provably at least half of N runs the streaming schedule
+# instead (a program of the same spec whose split parts exceed the register
+# capacity); measured, the streaming schedule is faster from about a third.
+STREAM_SHARE = 0.5
+STREAM_PART_ROWS = 4096     # streaming split part (rows) when it takes over
+
+
+def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
+    """Rows of an (n, b) call that the register-resident softmax surely
+    defers: segments longer than ``limit`` rows defer, so at least the
+    caller's longest segment when it exceeds the limit, and at least the rows
+    that B segments of at most ``limit`` rows cannot hold."""
+    if max_len is None or n <= 0 or limit <= 0:
+        return 0
+    return max(max_len if max_len > limit else 0, n - b * limit, 0)
+
 
 _torch_module = None
 
@@ -114,6 +135,7 @@ class CompiledProgram:
         self._workspaces: dict[tuple[int, int], Any] = {}
         self._names = {kernel["role"]: kernel["name"] for kernel in self._metadata["kernels"]}
         self._alone: int | None = None
+        self._wait_limit: dict[int, int] = {}   # device -> longest segment (rows) the register path holds
         self._torch_dtypes: tuple | None = None    # (values dtype, offsets dtype) as torch dtypes
         self._report_static: tuple | None = None   # (classes, thresholds) of every report
 
@@ -267,6 +289,48 @@ class CompiledProgram:
             self._alone = int(self._native_spec().alone_rows)
         return self._alone
 
+    def _streams(self, values, n: int, b: int, max_len: int | None) -> bool:
+        """Whether run(select="auto") takes the streaming schedule for this
+        register-resident softmax call (see STREAM_SHARE)."""
+        if not self._metadata["fused"] or max_len is None or n <= 0 or self.spec.debug_visits:
+            return False
+        try:
+            device = values.get_device()
+        except (AttributeError, RuntimeError):
+            return False
+        if not isinstance(device, int) or device < 0:
+            return False         # not a device tensor: validation reports it
+        limit = self._wait_limit.get(device)
+        if limit is None:
+            resident = self._module(device).resident_blocks("fused")
+            limit = self._wait_limit[device] = max(1, resident * 7 // 8) * int(self._metadata["part_rows"])
+        return deferred_rows_bound(n, b, max_len, limit) >= STREAM_SHARE * n
+
+    def _stream_module(self, device: int) -> native.NativeModule:
+        """The streaming schedule of this softmax: the same spec with split
+        parts beyond the register capacity (doubled until the library agrees)."""
+        key = (device, self._digest + ":stream")
+        module = _modules.get(key)
+        if module is not None:
+            return module
+        with _lock:
+            module = _modules.get(key)
+            if module is None:
+                self._module(device)     # the library check of the artifact
+                part_rows = max(STREAM_PART_ROWS, 2 * int(self._metadata["part_rows"]))
+                metadata = self._metadata
+                thresholds = metadata["thresholds"] or [-1, -1]
+                while True:
+                    spec = native.make_spec(self.spec.op, self.spec.dtype, self.spec.offsets_dtype,
+                                            self.spec.feature_dim, scale=self.spec.scale, mask=self.spec.mask,
+                                            vectorize=self.spec.optimizations.vectorize, t_wave=thresholds[0],
+                                            t_block=thresholds[1], part_rows=part_rows)
+                    if not native.uses_fused(spec):
+                        break
+                    part_rows *= 2
+                module = _modules[key] = native.NativeModule(device, spec)
+            return module
+
     def _plan(self, module: native.NativeModule, n: int, b: int, schedule: str) -> native.Plan:
         return self._plan_launches(module, n, b, schedule)[0]
 
@@ -278,7 +342,7 @@ class CompiledProgram:
             if len(self._plans) >= 256:
                 self._plans.clear()
                 self._launches.clear()
-            plan = self._plans[key] = module.plan(n, b, schedule)
+            plan = self._plans[key] = module.plan(n, b, "classified" if schedule == "stream" else schedule)
         launches = self._launches.get(key)
         if launches is None:
             steps = plan.steps
@@ -316,6 +380,13 @@ class CompiledProgram:
                     n, b = int(values.shape[0]), int(offsets.numel()) - 1
                 except (AttributeError, IndexError, TypeError):
                     n = b = None
+                if n is not None and self._streams(values, n, b, max_len):
+                    # Segments too long for the register-resident softmax
+                    # hold at least half the rows: the streaming schedule.
+                    selection = {"max_len": max_len, "streaming": True,
+                                 "reason": "segments too long to hold in registers carry at least half the rows"}
+                    return self._run(values, offsets, out, stream, mode, debug_buffers=debug_buffers, mask=mask,
+                                     selected="classified", selection=selection, max_len=max_len, streaming=True)
                 chosen, selection = (self.choose(n, b, max_len, device_l2_mib(values)) if n is not None
                                      else ("classified", {}))
             if chosen == "naive":
@@ -351,7 +422,7 @@ class CompiledProgram:
                 and 0 < self._alone_rows() and max_len <= self._alone_rows())
 
     def _run(self, values, offsets, out, stream, mode, *, debug_buffers, mask, selected, selection,
-             max_len: int | None = None) -> ExecutionReport:
+             max_len: int | None = None, streaming: bool = False) -> ExecutionReport:
         if mode not in ("validated", "checked"):
             raise ValidationError("mode must be validated or checked")
         if self.spec.mask != (mask is not None):
@@ -406,11 +477,13 @@ class CompiledProgram:
                 if b == 0:
                     return self._report(started, names, grids, 0, mode=mode, selected=selected, selection=selection,
                                         validation_bytes=validation_bytes, validation_ms=validation_ms)
-            short = self._short_segments(max_len)
+            short = not streaming and self._short_segments(max_len)
             if short:
                 selection = {**selection, "short_segments": True}
-            plan, plan_names, plan_grids, plan_ref = self._plan_launches(module, n, b,
-                                                                         "short" if short else self._schedule)
+            if streaming:
+                module = self._stream_module(device)
+            plan, plan_names, plan_grids, plan_ref = self._plan_launches(
+                module, n, b, "stream" if streaming else "short" if short else self._schedule)
             workspace = None
             if plan.workspace_bytes:
                 workspace = self._workspace(torch, values.device, active, int(plan.workspace_bytes),

@@ -211,3 +211,24 @@ def test_oracle_is_test_infrastructure_only():
     for path in (REPO / "ragged-mlir_amd" / "ragged").glob("*.py"):
         text = path.read_text()
         assert not re.search(r"^\s*(from|import)\s+oracle\b", text, flags=re.M), path.name
+
+
+def test_deferred_rows_bound_known_answers():
+    """Rows the register-resident softmax surely defers (segments longer than
+    its limit): the caller's longest segment when it exceeds the limit, or
+    the rows B segments of at most the limit cannot hold."""
+    from ragged.runtime import STREAM_SHARE, deferred_rows_bound
+    limit = 896 * 256
+    # Four 2^20-row segments: 4 x 2^20 - 4 x limit rows at least (and 2^20 from max_len).
+    assert deferred_rows_bound(4 << 20, 4, 1 << 20, limit) == (4 << 20) - 4 * limit
+    # C5: the longest segment (200,000 rows) fits; 8192 segments hold any N.
+    assert deferred_rows_bound(4_194_304, 8192, 200_000, limit) == 0
+    # One segment of half the rows beyond the limit.
+    assert deferred_rows_bound(8_388_608, 8193, 4_194_304, limit) == 4_194_304
+    assert deferred_rows_bound(8_388_608, 8193, 4_194_304, limit) >= STREAM_SHARE * 8_388_608
+    # A long segment that is a small share stays below the share.
+    assert deferred_rows_bound(5_194_304, 8193, 1_000_000, limit) < STREAM_SHARE * 5_194_304
+    # No max_len, an empty call or no limit: nothing is known.
+    assert deferred_rows_bound(4 << 20, 4, None, limit) == 0
+    assert deferred_rows_bound(0, 0, 5, limit) == 0
+    assert deferred_rows_bound(10, 1, 10, 0) == 0
