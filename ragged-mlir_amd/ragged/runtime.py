@@ -51,12 +51,15 @@ STREAM_PART_ROWS = 4096     # streaming split part (rows) when it takes over
 
 def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
     """Rows of an (n, b) call that the register-resident softmax surely
-    defers: segments longer than ``limit`` rows defer, so at least the
-    caller's longest segment when it exceeds the limit, and at least the rows
-    that B segments of at most ``limit`` rows cannot hold."""
+    defers: segments longer than ``limit`` rows defer, so at least the rows
+    that the segments of at most ``limit`` rows cannot hold -- N - B*limit,
+    or, when the caller's longest segment exceeds the limit (it is then one
+    of the deferred), the larger of it and N - (B-1)*limit."""
     if max_len is None or n <= 0 or limit <= 0:
         return 0
-    return max(max_len if max_len > limit else 0, n - b * limit, 0)
+    if max_len > limit:
+        return max(max_len, n - (b - 1) * limit)
+    return max(n - b * limit, 0)
 
 
 _torch_module = None

@@ -219,8 +219,13 @@ def test_deferred_rows_bound_known_answers():
     the rows B segments of at most the limit cannot hold."""
     from ragged.runtime import STREAM_SHARE, deferred_rows_bound
     limit = 896 * 256
-    # Four 2^20-row segments: 4 x 2^20 - 4 x limit rows at least (and 2^20 from max_len).
-    assert deferred_rows_bound(4 << 20, 4, 1 << 20, limit) == (4 << 20) - 4 * limit
+    # Four 2^20-row segments: the three others hold at most 3 x limit rows.
+    assert deferred_rows_bound(4 << 20, 4, 1 << 20, limit) == (4 << 20) - 3 * limit
+    # Sixteen 2^18-row segments (all beyond the limit, but only just): the bound is weak.
+    assert deferred_rows_bound(16 << 18, 16, 1 << 18, limit) == (16 << 18) - 15 * limit
+    assert deferred_rows_bound(16 << 18, 16, 1 << 18, limit) < STREAM_SHARE * (16 << 18)
+    # max_len within the limit: only what B segments of the limit cannot hold.
+    assert deferred_rows_bound(4 << 20, 4, limit, limit) == (4 << 20) - 4 * limit
     # C5: the longest segment (200,000 rows) fits; 8192 segments hold any N.
     assert deferred_rows_bound(4_194_304, 8192, 200_000, limit) == 0
     # One segment of half the rows beyond the limit.
