@@ -40,12 +40,15 @@ I64_MAX = 2**63 - 1
 # The register-resident softmax holds a segment's chunks only while the
 # device can hold them all: segments of more chunks than 7/8 of its resident
 # workgroups (the library's rule, rg_plan_create's wait_parts) defer every
-# chunk to the kernel's drain, which re-reads them about 3-4x slower per chunk
-# than the streaming worker's split schedule streams them. A call whose
-# deferred rows are provably at least half of N runs the streaming schedule
+# chunk to the kernel's drain, a pass per round of the resident workgroups
+# that re-reads them about 3-4x slower per chunk than the streaming worker's
+# split schedule streams them. A call whose deferred rows are provably at
+# least half of N and at least 1.5 such limits runs the streaming schedule
 # instead (a program of the same spec whose split parts exceed the register
-# capacity); measured, the streaming schedule is faster from about a third.
+# capacity). Measured with one long segment: at 1.1 limits the two schedules
+# are within 10% either way, from 2 limits streaming is 1.4-2.4x faster.
 STREAM_SHARE = 0.5
+STREAM_MIN_LIMITS = 1.5
 STREAM_PART_ROWS = 4096     # streaming split part (rows) when it takes over
 
 
@@ -60,6 +63,14 @@ def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
     if max_len > limit:
         return max(max_len, n - (b - 1) * limit)
     return max(n - b * limit, 0)
+
+
+def streams_long_segments(n: int, b: int, max_len: int | None, limit: int) -> bool:
+    """Whether a register-resident softmax call of (n, b, max_len) runs the
+    streaming schedule instead, given the longest segment ``limit`` (rows)
+    the register path holds."""
+    deferred = deferred_rows_bound(n, b, max_len, limit)
+    return deferred > 0 and deferred >= STREAM_SHARE * n and deferred >= STREAM_MIN_LIMITS * limit
 
 
 _torch_module = None
@@ -307,7 +318,7 @@ class CompiledProgram:
         if limit is None:
             resident = self._module(device).resident_blocks("fused")
             limit = self._wait_limit[device] = max(1, resident * 7 // 8) * int(self._metadata["part_rows"])
-        return deferred_rows_bound(n, b, max_len, limit) >= STREAM_SHARE * n
+        return streams_long_segments(n, b, max_len, limit)
 
     def _stream_module(self, device: int) -> native.NativeModule:
         """The streaming schedule of this softmax: the same spec with split
@@ -387,7 +398,8 @@ class CompiledProgram:
                     # Segments too long for the register-resident softmax
                     # hold at least half the rows: the streaming schedule.
                     selection = {"max_len": max_len, "streaming": True,
-                                 "reason": "segments too long to hold in registers carry at least half the rows"}
+                                 "reason": "segments too long to hold in registers carry at least half the rows "
+                                           "and 1.5 register limits"}
                     return self._run(values, offsets, out, stream, mode, debug_buffers=debug_buffers, mask=mask,
                                      selected="classified", selection=selection, max_len=max_len, streaming=True)
                 chosen, selection = (self.choose(n, b, max_len, device_l2_mib(values)) if n is not None

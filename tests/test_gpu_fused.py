@@ -181,15 +181,15 @@ def test_segments_beyond_the_resident_grid(artifact_cache, dtype, d, longest, sc
 def test_long_segments_take_the_streaming_schedule(artifact_cache, dtype, d, scale):
     """With max_len, run(select="auto") sends a register-resident softmax call
     whose segments too long to hold in registers surely carry at least half
-    the rows to the streaming worker's split schedule (classify + worker),
-    which matches the oracle; forced classified keeps the register-resident
-    kernel, and a long segment that is a small share of the rows stays
-    there too."""
+    the rows and 1.5 register limits to the streaming worker's split
+    schedule (classify + worker), which matches the oracle; forced classified
+    keeps the register-resident kernel, and a long segment that is a small
+    share of the rows stays there too."""
     kwargs = {"scale": scale} if scale != 1.0 else {}
     program = compile_softmax(artifact_cache, dtype, d, **kwargs)
     part = int(program.metadata["part_rows"])
     limit = max(1, module_of(program).resident_blocks("fused") * 7 // 8) * part
-    lengths = np.array([17, limit + 3 * part + 5, 3 * part, 0, 1], dtype=np.int64)
+    lengths = np.array([17, 2 * limit + 3 * part + 5, 3 * part, 0, 1], dtype=np.int64)
     offsets = offsets_from_lengths(lengths, "i64")
     values = np.random.default_rng(d).normal(size=(int(offsets[-1]), d)).astype(np.float32)
     max_len = int(lengths.max())

@@ -233,6 +233,16 @@ def test_deferred_rows_bound_known_answers():
     assert deferred_rows_bound(8_388_608, 8193, 4_194_304, limit) >= STREAM_SHARE * 8_388_608
     # A long segment that is a small share stays below the share.
     assert deferred_rows_bound(5_194_304, 8193, 1_000_000, limit) < STREAM_SHARE * 5_194_304
+    # The decision on the measured inputs: at least half the rows and 1.5 limits.
+    from ragged.runtime import streams_long_segments
+    assert streams_long_segments(4 << 20, 4, 1 << 20, limit)                       # 2.2x faster streamed
+    assert streams_long_segments(8_388_608, 8193, 4_194_304, limit)                # 1.5x
+    assert streams_long_segments(4 << 20, 8, 1 << 19, limit)                       # 2.2x
+    assert not streams_long_segments(4_194_304, 8192, 200_000, limit)              # C5
+    assert not streams_long_segments(5_194_304, 8193, 1_000_000, limit)            # a 19% segment
+    assert not streams_long_segments(131_072, 640, 114_860, 896 * 128)             # one round of the drain: 10% slower streamed
+    assert not streams_long_segments(int(1.1 * limit) + 517, 3, int(1.1 * limit), limit)   # within 10% either way
+    assert streams_long_segments(2 * limit + 517, 3, 2 * limit, limit)                     # 1.4-1.6x
     # No max_len, an empty call or no limit: nothing is known.
     assert deferred_rows_bound(4 << 20, 4, None, limit) == 0
     assert deferred_rows_bound(0, 0, 5, limit) == 0
