@@ -177,8 +177,9 @@ def test_segments_beyond_the_resident_grid(artifact_cache, dtype, d, longest, sc
         check(actual, values, offsets, op="softmax", dtype=dtype, scale=scale)
 
 
-@pytest.mark.parametrize("dtype,d,scale", [("bf16", 128, 1.0), ("bf16", 64, 0.5), ("f32", 128, 1.0)])
-def test_long_segments_take_the_streaming_schedule(artifact_cache, dtype, d, scale):
+@pytest.mark.parametrize("dtype,d,scale,masked", [("bf16", 128, 1.0, False), ("bf16", 64, 0.5, False),
+                                                  ("f32", 128, 1.0, False), ("bf16", 64, 1.0, True)])
+def test_long_segments_take_the_streaming_schedule(artifact_cache, dtype, d, scale, masked):
     """With max_len, run(select="auto") sends a register-resident softmax call
     whose segments too long to hold in registers surely carry at least half
     the rows and 1.5 register limits to the streaming worker's split
@@ -186,23 +187,29 @@ def test_long_segments_take_the_streaming_schedule(artifact_cache, dtype, d, sca
     keeps the register-resident kernel, and a long segment that is a small
     share of the rows stays there too."""
     kwargs = {"scale": scale} if scale != 1.0 else {}
+    if masked:
+        kwargs["mask"] = True
     program = compile_softmax(artifact_cache, dtype, d, **kwargs)
     part = int(program.metadata["part_rows"])
-    limit = max(1, module_of(program).resident_blocks("fused") * 7 // 8) * part
+    limit = max(1, program._module(0).resident_blocks("fused") * 7 // 8) * part
     lengths = np.array([17, 2 * limit + 3 * part + 5, 3 * part, 0, 1], dtype=np.int64)
     offsets = offsets_from_lengths(lengths, "i64")
-    values = np.random.default_rng(d).normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    rng = np.random.default_rng(d)
+    values = rng.normal(size=(int(offsets[-1]), d)).astype(np.float32)
+    mask = rng.normal(size=values.shape).astype(np.float32) if masked else None
     max_len = int(lengths.max())
     actual, report = run_program(program, values, offsets, dtype=dtype, op="softmax", select="auto",
-                                 max_len=max_len)
+                                 max_len=max_len, mask=mask)
     assert report.selection.get("streaming") and report.selected == "classified"
     assert not any("fused" in name for name in report.kernel_names), report.kernel_names
-    check(actual, values, offsets, op="softmax", dtype=dtype, scale=scale)
+    check(actual, values, offsets, op="softmax", dtype=dtype, scale=scale, mask=mask)
     actual, report = run_program(program, values, offsets, dtype=dtype, op="softmax", select="classified",
-                                 max_len=max_len)
+                                 max_len=max_len, mask=mask)
     assert not report.selection.get("streaming")
     assert any("fused" in name for name in report.kernel_names), report.kernel_names
-    check(actual, values, offsets, op="softmax", dtype=dtype, scale=scale)
+    check(actual, values, offsets, op="softmax", dtype=dtype, scale=scale, mask=mask)
+    if masked:
+        return
     # The long segment a third of the rows: register-resident (it defers that segment).
     short = np.array([limit + 5] + [part] * (2 * (limit + 5) // part + 1), dtype=np.int64)
     offsets = offsets_from_lengths(short, "i64")
