@@ -599,11 +599,11 @@ __global__ __launch_bounds__(kClassifyBlock) void k_classify(Params p) {
     long long total = 0;
     for (int w = 0; w < waves; ++w) total += run_s[c][w];
     // Run 3 is counted in counters[8]. A register-resident softmax
-    // (block_items set) counts run 0 in counters[7]: k_softmax_deferred
-    // takes the wave class, and k_softmax_fused, which reads counters[0],
-    // sees none. Its split reservations: direct chunks in counters[3], tree
-    // chunks (from the top of the item array) in counters[6], group rows in
-    // counters[kGroupRowSlot].
+    // (block_items set) counts run 0 in counters[7]: k_softmax_fused takes
+    // the wave class after its items from counters[7] and [8], and its item
+    // count, which adds counters[0], sees none. Its split reservations:
+    // direct chunks in counters[3], tree chunks (from the top of the item
+    // array) in counters[6], group rows in counters[kGroupRowSlot].
     const int slot = c == 3 ? 8 : c == 0 && p.block_items ? 7 : c == 4 ? 3 : c == 5 ? 6 : c == 6 ? kGroupRowSlot : c;
     long long base = total ? (long long)atomicAdd((unsigned long long*)(p.counters + slot), (unsigned long long)total) : 0;
     for (int w = 0; w < waves; ++w) {
