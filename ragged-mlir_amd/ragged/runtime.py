@@ -49,7 +49,24 @@ I64_MAX = 2**63 - 1
 # are within 10% either way, from 2 limits streaming is 1.4-2.4x faster.
 STREAM_SHARE = 0.5
 STREAM_MIN_LIMITS = 1.5
-STREAM_PART_ROWS = 4096     # streaming split part (rows) when it takes over
+# The streaming schedule's split parts when it takes over: about 2 MiB of rows,
+# at most 16,384 rows (measured, µs per call on four long-segment inputs:
+# f32 D=16 best at 16,384 rows = 1 MiB, f32 D=128 at 4,096 = 2 MiB, bf16 D=128
+# at 8,192 = 2 MiB, bf16 D=1024 at 1,024 = 2 MiB; a fixed 4,096 rows was up to
+# 1.9x slower).
+STREAM_PART_BYTES = 2 << 20
+STREAM_MAX_PART_ROWS = 16384
+
+
+def stream_part_rows(row_bytes: int, register_part_rows: int) -> int:
+    """Rows of a streaming split part for rows of ``row_bytes``: the power of
+    two nearest below STREAM_PART_BYTES of rows, at most STREAM_MAX_PART_ROWS,
+    and above the register path's part (so that the library runs the
+    streaming worker)."""
+    rows = 1
+    while rows * 2 * row_bytes <= STREAM_PART_BYTES and rows * 2 <= STREAM_MAX_PART_ROWS:
+        rows *= 2
+    return max(rows, 2 * register_part_rows)
 
 
 def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
@@ -322,7 +339,8 @@ class CompiledProgram:
 
     def _stream_module(self, device: int) -> native.NativeModule:
         """The streaming schedule of this softmax: the same spec with split
-        parts beyond the register capacity (doubled until the library agrees)."""
+        parts of about 2 MiB (``stream_part_rows``; doubled while the library
+        would still hold them in registers)."""
         key = (device, self._digest + ":stream")
         module = _modules.get(key)
         if module is not None:
@@ -331,7 +349,8 @@ class CompiledProgram:
             module = _modules.get(key)
             if module is None:
                 self._module(device)     # the library check of the artifact
-                part_rows = max(STREAM_PART_ROWS, 2 * int(self._metadata["part_rows"]))
+                row_bytes = self.spec.feature_dim * (2 if self.spec.dtype == "bf16" else 4)
+                part_rows = stream_part_rows(row_bytes, int(self._metadata["part_rows"]))
                 metadata = self._metadata
                 thresholds = metadata["thresholds"] or [-1, -1]
                 while True:

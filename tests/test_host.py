@@ -247,3 +247,15 @@ def test_deferred_rows_bound_known_answers():
     assert deferred_rows_bound(4 << 20, 4, None, limit) == 0
     assert deferred_rows_bound(0, 0, 5, limit) == 0
     assert deferred_rows_bound(10, 1, 10, 0) == 0
+
+
+def test_stream_part_rows_known_answers():
+    """Streaming split parts of about 2 MiB of rows, at most 16,384 rows, and
+    beyond the register path's part."""
+    from ragged.runtime import stream_part_rows
+    assert stream_part_rows(16 * 4, 1024) == 16384          # f32 D=16: 1 MiB (the row cap)
+    assert stream_part_rows(128 * 4, 128) == 4096           # f32 D=128: 2 MiB
+    assert stream_part_rows(128 * 2, 256) == 8192           # bf16 D=128: 2 MiB
+    assert stream_part_rows(1024 * 2, 32) == 1024           # bf16 D=1024: 2 MiB
+    assert stream_part_rows(4096 * 4, 8) == 128             # f32 D=4096: 2 MiB
+    assert stream_part_rows(128 * 2, 16384) == 32768        # beyond a (hypothetical) large register part
