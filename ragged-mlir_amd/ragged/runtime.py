@@ -82,6 +82,32 @@ def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
     return max(n - b * limit, 0)
 
 
+# Sum / max calls of at least BIG_REDUCE_BYTES of rows (beyond every
+# calibration suite, whose reduce inputs stay below about 300 MiB) split long
+# segments into parts of about N/512 rows (at most 4 MiB) instead of the
+# library's 256 KiB: every part publishes its partial with a release (an L2
+# write-back) and counts in at its segment, so thousands of small parts cost
+# more than the bandwidth they add. Measured (µs per call, default -> these
+# parts): f32 D=128 one 2^22-row segment 2,430 -> 463, 64 segments of 2^16
+# rows 764 -> 413; bf16 D=128 four 2^20-row segments 551 -> 221.
+BIG_REDUCE_BYTES = 1 << 30
+BIG_PART_SHARE = 512
+BIG_PART_BYTES = 4 << 20
+
+
+def big_part_rows(n: int, row_bytes: int, default_rows: int) -> int:
+    """Split part (rows) of a sum / max call of ``n`` rows of ``row_bytes``
+    (the library's default below BIG_REDUCE_BYTES): the power of two nearest
+    below n / BIG_PART_SHARE, at most BIG_PART_BYTES of rows, at least the
+    default."""
+    if n * row_bytes < BIG_REDUCE_BYTES:
+        return default_rows
+    rows = default_rows
+    while rows * 2 <= n // BIG_PART_SHARE and rows * 2 * row_bytes <= BIG_PART_BYTES:
+        rows *= 2
+    return rows
+
+
 def streams_long_segments(n: int, b: int, max_len: int | None, limit: int) -> bool:
     """Whether a register-resident softmax call of (n, b, max_len) runs the
     streaming schedule instead, given the longest segment ``limit`` (rows)
@@ -364,6 +390,23 @@ class CompiledProgram:
                 module = _modules[key] = native.NativeModule(device, spec)
             return module
 
+    def _parts_module(self, device: int, part_rows: int) -> native.NativeModule:
+        """This sum / max program with split parts of ``part_rows`` rows
+        (``big_part_rows``)."""
+        key = (device, f"{self._digest}:parts{part_rows}")
+        module = _modules.get(key)
+        if module is not None:
+            return module
+        with _lock:
+            module = _modules.get(key)
+            if module is None:
+                spec = self._native_spec()
+                module = _modules[key] = native.NativeModule(device, native.make_spec(
+                    self.spec.op, self.spec.dtype, self.spec.offsets_dtype, self.spec.feature_dim,
+                    vectorize=self.spec.optimizations.vectorize, t_wave=int(spec.t_wave), t_block=int(spec.t_block),
+                    part_rows=part_rows))
+            return module
+
     def _plan(self, module: native.NativeModule, n: int, b: int, schedule: str) -> native.Plan:
         return self._plan_launches(module, n, b, schedule)[0]
 
@@ -375,7 +418,8 @@ class CompiledProgram:
             if len(self._plans) >= 256:
                 self._plans.clear()
                 self._launches.clear()
-            plan = self._plans[key] = module.plan(n, b, "classified" if schedule == "stream" else schedule)
+            native_schedule = "classified" if schedule == "stream" or schedule.startswith("parts") else schedule
+            plan = self._plans[key] = module.plan(n, b, native_schedule)
         launches = self._launches.get(key)
         if launches is None:
             steps = plan.steps
@@ -514,10 +558,18 @@ class CompiledProgram:
             short = not streaming and self._short_segments(max_len)
             if short:
                 selection = {**selection, "short_segments": True}
+            schedule = "stream" if streaming else "short" if short else self._schedule
             if streaming:
                 module = self._stream_module(device)
-            plan, plan_names, plan_grids, plan_ref = self._plan_launches(
-                module, n, b, "stream" if streaming else "short" if short else self._schedule)
+            elif schedule == "classified" and self.spec.op != "softmax" and not self.spec.debug_visits:
+                default_rows = int(self._metadata["part_rows"])
+                part_rows = big_part_rows(n, self.spec.feature_dim * (2 if self.spec.dtype == "bf16" else 4),
+                                          default_rows)
+                if part_rows != default_rows:
+                    module = self._parts_module(device, part_rows)
+                    schedule = f"parts{part_rows}"
+                    selection = {**selection, "part_rows": part_rows}
+            plan, plan_names, plan_grids, plan_ref = self._plan_launches(module, n, b, schedule)
             workspace = None
             if plan.workspace_bytes:
                 workspace = self._workspace(torch, values.device, active, int(plan.workspace_bytes),

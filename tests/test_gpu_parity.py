@@ -424,3 +424,29 @@ def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
     print(f"split parts deferred to the last workgroup: {deferred}")
     check(actual, values, offsets, op="softmax", dtype=dtype, mask=mask, scale=1.25 if masked else 1.0)
     assert np.array_equal(actual, baseline, equal_nan=True)
+
+
+@pytest.mark.parametrize("op", ["sum", "max"])
+def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op):
+    """Sum / max calls of at least runtime.BIG_REDUCE_BYTES of rows split long
+    segments into parts of about N/512 rows (a companion module); lowered
+    here so that a 470 MB call takes them, the result matches the oracle
+    (max bit-exact) and the report names the part size; forced naive and a
+    call below the bound keep the default."""
+    from ragged import runtime
+    from ragged.workloads import offsets_from_lengths
+    from gpu_helpers import check, run_program
+    monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 20)
+    program = Compiler().compile(ProgramSpec(op, "f32", 128, "i64"), artifact_cache)
+    default_rows = int(program.metadata["part_rows"])
+    lengths = np.array([(1 << 19) + (1 << 18), 1 << 17, 100, 0, 7], dtype=np.int64)
+    offsets = offsets_from_lengths(lengths, "i64")
+    values = np.random.default_rng(5).normal(size=(int(offsets[-1]), 128)).astype(np.float32)
+    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
+    assert report.selection.get("part_rows") == runtime.big_part_rows(int(offsets[-1]), 512, default_rows)
+    assert report.selection["part_rows"] > default_rows
+    check(actual, values, offsets, op=op, dtype="f32")
+    monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 40)
+    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
+    assert "part_rows" not in report.selection
+    check(actual, values, offsets, op=op, dtype="f32")

@@ -259,3 +259,16 @@ def test_stream_part_rows_known_answers():
     assert stream_part_rows(1024 * 2, 32) == 1024           # bf16 D=1024: 2 MiB
     assert stream_part_rows(4096 * 4, 8) == 128             # f32 D=4096: 2 MiB
     assert stream_part_rows(128 * 2, 16384) == 32768        # beyond a (hypothetical) large register part
+
+
+def test_big_part_rows_known_answers():
+    """Sum / max calls of at least 1 GiB of rows split into parts of about
+    N/512 rows, at most 4 MiB, at least the library's default; smaller calls
+    keep the default."""
+    from ragged.runtime import big_part_rows
+    assert big_part_rows(1 << 22, 512, 512) == 8192          # f32 D=128, 2 GiB: 4 MiB parts
+    assert big_part_rows(1 << 22, 256, 1024) == 8192         # bf16 D=128, 1 GiB: 2 MiB parts
+    assert big_part_rows(1 << 24, 512, 512) == 8192          # 8 GiB: capped at 4 MiB
+    assert big_part_rows(1 << 21, 256, 1024) == 1024         # 512 MiB: the default
+    assert big_part_rows(1_040_746, 512, 512) == 512         # C2 (533 MB): the default
+    assert big_part_rows(1 << 27, 8, 32768) == 262144        # f32 D=2, 1 GiB: N/512 rows (2 MiB)
