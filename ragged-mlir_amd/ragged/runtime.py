@@ -83,14 +83,17 @@ def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
 
 
 # Sum / max calls of at least BIG_REDUCE_BYTES of rows (beyond every
-# calibration suite, whose reduce inputs stay below about 300 MiB) split long
+# calibration suite, whose largest reduce input is 304 MiB) split long
 # segments into parts of about N/512 rows (at most 4 MiB) instead of the
-# library's 256 KiB: every part publishes its partial with a release (an L2
-# write-back) and counts in at its segment, so thousands of small parts cost
-# more than the bandwidth they add. Measured (µs per call, default -> these
-# parts): f32 D=128 one 2^22-row segment 2,430 -> 463, 64 segments of 2^16
-# rows 764 -> 413; bf16 D=128 four 2^20-row segments 551 -> 221.
-BIG_REDUCE_BYTES = 1 << 30
+# library's 256 KiB: every part is a queue item that publishes its partial
+# with a release (an L2 write-back) and counts in at its segment, and
+# thousands of small ones cost more than the parallelism they add. Measured
+# (µs per call, default -> these parts): f32 D=128 one 2^22-row segment
+# 2,430 -> 463, 64 segments of 2^16 rows 764 -> 413, three 2^18-row segments
+# (384 MiB) 215 -> 134; bf16 D=128 four 2^20-row segments 551 -> 221. Only
+# calls that provably hold a segment longer than the block class take them
+# (``splits_segments``).
+BIG_REDUCE_BYTES = 320 << 20
 BIG_PART_SHARE = 512
 BIG_PART_BYTES = 4 << 20
 
@@ -106,6 +109,13 @@ def big_part_rows(n: int, row_bytes: int, default_rows: int) -> int:
     while rows * 2 <= n // BIG_PART_SHARE and rows * 2 * row_bytes <= BIG_PART_BYTES:
         rows *= 2
     return rows
+
+
+def splits_segments(n: int, b: int, max_len: int | None, t_block: int) -> bool:
+    """Whether a call of (n, b, max_len) provably holds a segment longer than
+    the block class (``t_block`` rows): by max_len, or else by more rows than
+    b block-class segments hold."""
+    return max_len > t_block if max_len is not None else n > b * t_block
 
 
 def streams_long_segments(n: int, b: int, max_len: int | None, limit: int) -> bool:
@@ -565,7 +575,10 @@ class CompiledProgram:
                 default_rows = int(self._metadata["part_rows"])
                 part_rows = big_part_rows(n, self.spec.feature_dim * (2 if self.spec.dtype == "bf16" else 4),
                                           default_rows)
-                if part_rows != default_rows:
+                # Part size matters only where a segment is longer than the
+                # block class.
+                if part_rows != default_rows and splits_segments(n, b, max_len,
+                                                                 int(self._metadata["thresholds"][1])):
                     module = self._parts_module(device, part_rows)
                     schedule = f"parts{part_rows}"
                     selection = {**selection, "part_rows": part_rows}

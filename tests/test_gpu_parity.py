@@ -429,23 +429,32 @@ def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
 @pytest.mark.parametrize("op", ["sum", "max"])
 def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op):
     """Sum / max calls of at least runtime.BIG_REDUCE_BYTES of rows split long
-    segments into parts of about N/512 rows (a companion module); lowered
-    here so that a 470 MB call takes them, the result matches the oracle
-    (max bit-exact) and the report names the part size; forced naive and a
-    call below the bound keep the default."""
+    segments into parts of about N/512 rows (a companion module); lowered here
+    so that a 690 MB call takes them, the result matches the oracle (max
+    bit-exact) and the report names the part size; a call whose max_len fits
+    the block class and a call below the bound keep the default."""
     from ragged import runtime
     from ragged.workloads import offsets_from_lengths
     from gpu_helpers import check, run_program
     monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 20)
     program = Compiler().compile(ProgramSpec(op, "f32", 128, "i64"), artifact_cache)
     default_rows = int(program.metadata["part_rows"])
-    lengths = np.array([(1 << 19) + (1 << 18), 1 << 17, 100, 0, 7], dtype=np.int64)
+    default_block = int(program.metadata["thresholds"][1])
+    # Segments of one, two and three 2048-row parts around the block class.
+    lengths = np.array([(1 << 20) + (1 << 18), 1 << 17, 2049, 2048, 1500, 1025, default_block, 100, 0, 7],
+                       dtype=np.int64)
     offsets = offsets_from_lengths(lengths, "i64")
     values = np.random.default_rng(5).normal(size=(int(offsets[-1]), 128)).astype(np.float32)
     actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
-    assert report.selection.get("part_rows") == runtime.big_part_rows(int(offsets[-1]), 512, default_rows)
-    assert report.selection["part_rows"] > default_rows
+    rows = runtime.big_part_rows(int(offsets[-1]), 512, default_rows)
+    assert report.selection.get("part_rows") == rows == 2048 > default_rows
     check(actual, values, offsets, op=op, dtype="f32")
+    short = offsets_from_lengths(np.array([default_block] * 4 + [3], dtype=np.int64), "i64")
+    few = values[:int(short[-1])]
+    actual, report = run_program(program, few, short, dtype="f32", op=op, select="classified",
+                                 max_len=default_block)
+    assert "part_rows" not in report.selection
+    check(actual, few, short, op=op, dtype="f32")
     monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 40)
     actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
     assert "part_rows" not in report.selection

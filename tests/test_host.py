@@ -262,13 +262,31 @@ def test_stream_part_rows_known_answers():
 
 
 def test_big_part_rows_known_answers():
-    """Sum / max calls of at least 1 GiB of rows split into parts of about
+    """Sum / max calls of at least 320 MiB of rows split into parts of about
     N/512 rows, at most 4 MiB, at least the library's default; smaller calls
-    keep the default."""
+    (every calibration suite's, at most 304 MiB) keep the default."""
     from ragged.runtime import big_part_rows
     assert big_part_rows(1 << 22, 512, 512) == 8192          # f32 D=128, 2 GiB: 4 MiB parts
     assert big_part_rows(1 << 22, 256, 1024) == 8192         # bf16 D=128, 1 GiB: 2 MiB parts
     assert big_part_rows(1 << 24, 512, 512) == 8192          # 8 GiB: capped at 4 MiB
-    assert big_part_rows(1 << 21, 256, 1024) == 1024         # 512 MiB: the default
-    assert big_part_rows(1_040_746, 512, 512) == 512         # C2 (533 MB): the default
+    assert big_part_rows(1 << 21, 256, 1024) == 4096         # bf16 D=128, 512 MiB: 1 MiB parts
+    assert big_part_rows(1_040_746, 512, 512) == 1024        # C2 (508 MiB): 2032 rows per 512th -> 1024
+    assert big_part_rows(655_360, 512, 512) == 1024          # f32 D=128, exactly 320 MiB
+    assert big_part_rows(655_359, 512, 512) == 512           # one row less: the default
+    assert big_part_rows(1 << 20, 304, 862) == 862           # the suites' largest (f32 D=76, 304 MiB)
     assert big_part_rows(1 << 27, 8, 32768) == 262144        # f32 D=2, 1 GiB: N/512 rows (2 MiB)
+
+
+def test_splits_segments_known_answers():
+    """Larger split parts are taken only by calls that provably hold a
+    segment longer than the block class: by max_len, or without it by more
+    rows than b block-class segments hold (pigeonhole)."""
+    from ragged.runtime import splits_segments
+    assert not splits_segments(1_040_746, 4096, None, 1024)   # C2 without max_len: 4096 x 1024 rows would hold it
+    assert not splits_segments(1_040_746, 4096, 512, 1024)    # C2 with max_len
+    assert splits_segments(786_432, 3, None, 1024)             # three 2^18-row segments
+    assert splits_segments(3073, 3, None, 1024)                # one row more than three block segments hold
+    assert not splits_segments(3072, 3, None, 1024)            # could be three 1024-row segments
+    assert splits_segments(4_194_304, 8192, 200_000, 1024)     # C5 lengths with max_len
+    assert not splits_segments(4_194_304, 8192, None, 1024)    # ... and without: not provable
+    assert not splits_segments(0, 0, None, 1024)
