@@ -430,7 +430,7 @@ def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
 def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op):
     """Sum / max calls of at least runtime.BIG_REDUCE_BYTES of rows split long
     segments into parts of about N/512 rows (a companion module); lowered here
-    so that a 690 MB call takes them, the result matches the oracle (max
+    so that a 742 MB call takes them, the result matches the oracle (max
     bit-exact) and the report names the part size; a call whose max_len fits
     the block class and a call below the bound keep the default."""
     from ragged import runtime
