@@ -358,7 +358,7 @@ def run_config(name: str, args, torch, cache, seed: int = 711) -> list[dict]:
             module.profile_start(args.steps)
             timed_calls()
             profile = module.profile_stop()
-            plan = next(v for k, v in chosen._plans.items() if k[:3] == (0, workload.n, workload.b))
+            plan = next(v for k, v in chosen._plans.items() if k[0] is module and k[1:3] == (workload.n, workload.b))
             total_bytes = algorithmic_bytes(op, workload.n, workload.b, workload.d, element, offset_bytes)
             kernels = {}
             for role, entry in profile["roles"].items():

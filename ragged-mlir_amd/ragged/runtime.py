@@ -92,10 +92,12 @@ def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
 # 2,430 -> 463, 64 segments of 2^16 rows 764 -> 413, three 2^18-row segments
 # (384 MiB) 215 -> 134; bf16 D=128 four 2^20-row segments 551 -> 221. Only
 # calls that provably hold a segment longer than the block class take them
-# (``splits_segments``).
+# (``splits_segments``), and segments one part would hold join the block
+# class (``big_block_rows``).
 BIG_REDUCE_BYTES = 320 << 20
 BIG_PART_SHARE = 512
 BIG_PART_BYTES = 4 << 20
+BIG_BLOCK_SHARE = 1024
 
 
 def big_part_rows(n: int, row_bytes: int, default_rows: int) -> int:
@@ -109,6 +111,16 @@ def big_part_rows(n: int, row_bytes: int, default_rows: int) -> int:
     while rows * 2 <= n // BIG_PART_SHARE and rows * 2 * row_bytes <= BIG_PART_BYTES:
         rows *= 2
     return rows
+
+
+def big_block_rows(n: int, part_rows: int, default_t_block: int) -> int:
+    """Longest block-class segment of a call of ``n`` rows that splits into
+    ``part_rows`` parts: a segment one part would hold goes to one workgroup
+    whole, with no partial to publish (as one split part it costs 1.2-1.3x
+    the time), up to n / BIG_BLOCK_SHARE rows (about 1.5 resident
+    workgroups' share of the call: block items are taken after the split
+    parts, and larger ones finish last)."""
+    return max(default_t_block, min(part_rows, n // BIG_BLOCK_SHARE))
 
 
 def splits_segments(n: int, b: int, max_len: int | None, t_block: int) -> bool:
@@ -193,10 +205,10 @@ class CompiledProgram:
             raise CacheMismatch("a block-per-segment companion must be the naive strategy of a classifying program")
         self.naive = naive
         self._choices: dict[tuple, tuple[str, dict[str, Any]]] = {}
-        self._plans: dict[tuple[int, int, int, str], native.Plan] = {}
+        self._plans: dict[tuple[native.NativeModule, int, int, str], native.Plan] = {}
         # Per plan: its kernel names and grids for reports, and the ctypes
         # reference rg_run takes (built once, not per call).
-        self._launches: dict[tuple[int, int, int, str], tuple[list, list, Any]] = {}
+        self._launches: dict[tuple[native.NativeModule, int, int, str], tuple[list, list, Any]] = {}
         # Workspace per (device, stream): calls on one stream run in order,
         # so they can share it; it grows to the largest plan seen.
         self._workspaces: dict[tuple[int, int], Any] = {}
@@ -236,6 +248,7 @@ class CompiledProgram:
         """Drop this program's plans and workspaces; the shared native module
         stays loaded."""
         self._plans.clear()
+        self._launches.clear()
         self._workspaces.clear()
 
     def _workspace(self, torch, device, stream, nbytes: int, fresh: bool):
@@ -400,10 +413,11 @@ class CompiledProgram:
                 module = _modules[key] = native.NativeModule(device, spec)
             return module
 
-    def _parts_module(self, device: int, part_rows: int) -> native.NativeModule:
-        """This sum / max program with split parts of ``part_rows`` rows
-        (``big_part_rows``)."""
-        key = (device, f"{self._digest}:parts{part_rows}")
+    def _parts_module(self, device: int, part_rows: int, t_block: int) -> native.NativeModule:
+        """This sum / max program with split parts of ``part_rows`` rows and
+        block-class segments up to ``t_block`` rows (``big_part_rows``,
+        ``big_block_rows``)."""
+        key = (device, f"{self._digest}:parts{part_rows}:block{t_block}")
         module = _modules.get(key)
         if module is not None:
             return module
@@ -413,7 +427,7 @@ class CompiledProgram:
                 spec = self._native_spec()
                 module = _modules[key] = native.NativeModule(device, native.make_spec(
                     self.spec.op, self.spec.dtype, self.spec.offsets_dtype, self.spec.feature_dim,
-                    vectorize=self.spec.optimizations.vectorize, t_wave=int(spec.t_wave), t_block=int(spec.t_block),
+                    vectorize=self.spec.optimizations.vectorize, t_wave=int(spec.t_wave), t_block=t_block,
                     part_rows=part_rows))
             return module
 
@@ -421,8 +435,10 @@ class CompiledProgram:
         return self._plan_launches(module, n, b, schedule)[0]
 
     def _plan_launches(self, module: native.NativeModule, n: int, b: int, schedule: str):
-        """(plan, kernel names, grids, ctypes reference) for (N, B, schedule)."""
-        key = (module.device, n, b, schedule)
+        """(plan, kernel names, grids, ctypes reference) for (N, B, schedule)
+        on ``module``: keyed by the module, whose thresholds and part size the
+        plan carries."""
+        key = (module, n, b, schedule)
         plan = self._plans.get(key)
         if plan is None:
             if len(self._plans) >= 256:
@@ -491,8 +507,12 @@ class CompiledProgram:
         static = self._report_static
         if static is None:
             static = self._report_static = (tuple(metadata["classes"]), tuple(metadata["thresholds"]))
+        thresholds = static[1]
+        if selection and "t_block" in selection:
+            # A companion module's block threshold (big_block_rows).
+            thresholds = (thresholds[0], selection["t_block"]) + thresholds[2:]
         return ExecutionReport(
-            static[0] if plan_names else (), static[1], tuple(grids),
+            static[0] if plan_names else (), thresholds, tuple(grids),
             workspace + validation_bytes, self._digest, None, mode, tuple(plan_names),
             (time.perf_counter() - started) * 1000, cache_hit=self.cache_hit,
             validation_workspace_bytes=validation_bytes, validation_host_ms=validation_ms,
@@ -577,11 +597,12 @@ class CompiledProgram:
                                           default_rows)
                 # Part size matters only where a segment is longer than the
                 # block class.
-                if part_rows != default_rows and splits_segments(n, b, max_len,
-                                                                 int(self._metadata["thresholds"][1])):
-                    module = self._parts_module(device, part_rows)
+                default_block = int(self._metadata["thresholds"][1])
+                if part_rows != default_rows and splits_segments(n, b, max_len, default_block):
+                    t_block = big_block_rows(n, part_rows, default_block)
+                    module = self._parts_module(device, part_rows, t_block)
                     schedule = f"parts{part_rows}"
-                    selection = {**selection, "part_rows": part_rows}
+                    selection = {**selection, "part_rows": part_rows, "t_block": t_block}
             plan, plan_names, plan_grids, plan_ref = self._plan_launches(module, n, b, schedule)
             workspace = None
             if plan.workspace_bytes:

@@ -429,10 +429,13 @@ def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
 @pytest.mark.parametrize("op", ["sum", "max"])
 def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op):
     """Sum / max calls of at least runtime.BIG_REDUCE_BYTES of rows split long
-    segments into parts of about N/512 rows (a companion module); lowered here
-    so that a 742 MB call takes them, the result matches the oracle (max
-    bit-exact) and the report names the part size; a call whose max_len fits
-    the block class and a call below the bound keep the default."""
+    segments into parts of about N/512 rows and send segments of up to N/1024
+    rows to the block class (a companion module); lowered here so that a 742 MB
+    call takes them, the result matches the oracle (max bit-exact) and the
+    report names the part size and block threshold. The same (N, B) on a
+    module with another block threshold gets a plan of its own (plans are
+    keyed by module). A call whose max_len fits the block class and a call
+    below the bound keep the default."""
     from ragged import runtime
     from ragged.workloads import offsets_from_lengths
     from gpu_helpers import check, run_program
@@ -440,7 +443,8 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
     program = Compiler().compile(ProgramSpec(op, "f32", 128, "i64"), artifact_cache)
     default_rows = int(program.metadata["part_rows"])
     default_block = int(program.metadata["thresholds"][1])
-    # Segments of one, two and three 2048-row parts around the block class.
+    # Around the default block threshold (1,024 rows), the raised one (1,415)
+    # and the part (2,048): block, one split part, two parts.
     lengths = np.array([(1 << 20) + (1 << 18), 1 << 17, 2049, 2048, 1500, 1025, default_block, 100, 0, 7],
                        dtype=np.int64)
     offsets = offsets_from_lengths(lengths, "i64")
@@ -448,12 +452,23 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
     actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
     rows = runtime.big_part_rows(int(offsets[-1]), 512, default_rows)
     assert report.selection.get("part_rows") == rows == 2048 > default_rows
+    t_block = runtime.big_block_rows(int(offsets[-1]), rows, default_block)
+    assert report.selection["t_block"] == report.thresholds[1] == t_block == 1415
     check(actual, values, offsets, op=op, dtype="f32")
+    shipped = runtime.big_block_rows
+    monkeypatch.setattr(runtime, "big_block_rows", lambda n, part_rows, default_t_block: default_t_block)
+    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
+    assert report.selection["t_block"] == report.thresholds[1] == default_block
+    plans = {int(plan.t_block) for (module, n, b, schedule), plan in program._plans.items()
+             if (n, b, schedule) == (int(offsets[-1]), len(lengths), f"parts{rows}")}
+    assert plans == {default_block, t_block}
+    check(actual, values, offsets, op=op, dtype="f32")
+    monkeypatch.setattr(runtime, "big_block_rows", shipped)
     short = offsets_from_lengths(np.array([default_block] * 4 + [3], dtype=np.int64), "i64")
     few = values[:int(short[-1])]
     actual, report = run_program(program, few, short, dtype="f32", op=op, select="classified",
                                  max_len=default_block)
-    assert "part_rows" not in report.selection
+    assert "part_rows" not in report.selection and report.thresholds[1] == default_block
     check(actual, few, short, op=op, dtype="f32")
     monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 40)
     actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
