@@ -82,31 +82,29 @@ def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
     return max(n - b * limit, 0)
 
 
-# Sum / max calls of at least BIG_REDUCE_BYTES of rows (beyond every
-# calibration suite, whose largest reduce input is 304 MiB) split long
-# segments into parts of about N/512 rows (at most 4 MiB) instead of the
-# library's 256 KiB: every part is a queue item that publishes its partial
-# with a release (an L2 write-back) and counts in at its segment, and
-# thousands of small ones cost more than the parallelism they add. Measured
-# (µs per call, default -> these parts): f32 D=128 one 2^22-row segment
-# 2,430 -> 463, 64 segments of 2^16 rows 764 -> 413, three 2^18-row segments
-# (384 MiB) 215 -> 134; bf16 D=128 four 2^20-row segments 551 -> 221. Only
-# calls that provably hold a segment longer than the block class take them
-# (``splits_segments``), and segments one part would hold join the block
-# class (``big_block_rows``).
-BIG_REDUCE_BYTES = 320 << 20
+# Sum / max calls split long segments into parts of about N/512 rows (at
+# most 4 MiB) instead of the library's 256 KiB once N/512 rows reach twice the
+# default part (from about 256 MiB of rows): every part is a queue item that
+# publishes its partial with a release (an L2 write-back) and counts in at its
+# segment, and thousands of small ones cost more than the parallelism they
+# add. Measured (µs per call, default -> these parts and block class): f32
+# D=128 one 2^22-row segment 2,438 -> 466, 64 segments of 2^16 rows 783 ->
+# 420, three 2^18-row segments (384 MiB) 219 -> 133; bf16 D=128 four 2^20-row
+# segments 546 -> 233; on the calibration suites' 32 training cases it
+# changes, 11% less time warm. Only calls that provably hold a segment longer
+# than the block class take them (``splits_segments``), and segments of up to
+# N/1024 rows join the block class (``big_block_rows``). The cost model was
+# fitted on measurements taken with these rules.
 BIG_PART_SHARE = 512
 BIG_PART_BYTES = 4 << 20
 BIG_BLOCK_SHARE = 1024
 
 
 def big_part_rows(n: int, row_bytes: int, default_rows: int) -> int:
-    """Split part (rows) of a sum / max call of ``n`` rows of ``row_bytes``
-    (the library's default below BIG_REDUCE_BYTES): the power of two nearest
-    below n / BIG_PART_SHARE, at most BIG_PART_BYTES of rows, at least the
-    default."""
-    if n * row_bytes < BIG_REDUCE_BYTES:
-        return default_rows
+    """Split part (rows) of a sum / max call of ``n`` rows of ``row_bytes``:
+    the power of two nearest below n / BIG_PART_SHARE, at most BIG_PART_BYTES
+    of rows, at least the library's default (which it stays while
+    n / BIG_PART_SHARE is below twice the default)."""
     rows = default_rows
     while rows * 2 <= n // BIG_PART_SHARE and rows * 2 * row_bytes <= BIG_PART_BYTES:
         rows *= 2

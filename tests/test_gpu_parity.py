@@ -428,18 +428,16 @@ def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
 
 @pytest.mark.parametrize("op", ["sum", "max"])
 def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op):
-    """Sum / max calls of at least runtime.BIG_REDUCE_BYTES of rows split long
-    segments into parts of about N/512 rows and send segments of up to N/1024
-    rows to the block class (a companion module); lowered here so that a 742 MB
-    call takes them, the result matches the oracle (max bit-exact) and the
-    report names the part size and block threshold. The same (N, B) on a
-    module with another block threshold gets a plan of its own (plans are
-    keyed by module). A call whose max_len fits the block class and a call
-    below the bound keep the default."""
+    """Sum / max calls of more than about 256 MiB of rows split long segments
+    into parts of about N/512 rows and send segments of up to N/1024 rows to
+    the block class (a companion module): on a 742 MB call the result matches
+    the oracle (max bit-exact) and the report names the part size and block
+    threshold. The same (N, B) on a module with another block threshold gets
+    a plan of its own (plans are keyed by module). A call whose max_len fits
+    the block class and a small call keep the default."""
     from ragged import runtime
     from ragged.workloads import offsets_from_lengths
     from gpu_helpers import check, run_program
-    monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 20)
     program = Compiler().compile(ProgramSpec(op, "f32", 128, "i64"), artifact_cache)
     default_rows = int(program.metadata["part_rows"])
     default_block = int(program.metadata["thresholds"][1])
@@ -470,7 +468,9 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
                                  max_len=default_block)
     assert "part_rows" not in report.selection and report.thresholds[1] == default_block
     check(actual, few, short, op=op, dtype="f32")
-    monkeypatch.setattr(runtime, "BIG_REDUCE_BYTES", 1 << 40)
-    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
+    # A small call that provably splits a segment: N/512 is below twice the
+    # default part.
+    small = offsets_from_lengths(np.array([3000, 3], dtype=np.int64), "i64")
+    actual, report = run_program(program, values[:3003], small, dtype="f32", op=op, select="classified")
     assert "part_rows" not in report.selection
-    check(actual, values, offsets, op=op, dtype="f32")
+    check(actual, values[:3003], small, op=op, dtype="f32")

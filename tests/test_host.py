@@ -262,19 +262,20 @@ def test_stream_part_rows_known_answers():
 
 
 def test_big_part_rows_known_answers():
-    """Sum / max calls of at least 320 MiB of rows split into parts of about
-    N/512 rows, at most 4 MiB, at least the library's default; smaller calls
-    (every calibration suite's, at most 304 MiB) keep the default. Segments
-    one such part holds go to the block class."""
+    """Sum / max calls split into parts of about N/512 rows, at most 4 MiB,
+    at least the library's default, which they keep while N/512 is below
+    twice it (about 256 MiB of rows). Segments of up to N/1024 rows (at most
+    a part) go to the block class."""
     from ragged.runtime import big_block_rows, big_part_rows
     assert big_part_rows(1 << 22, 512, 512) == 8192          # f32 D=128, 2 GiB: 4 MiB parts
     assert big_part_rows(1 << 22, 256, 1024) == 8192         # bf16 D=128, 1 GiB: 2 MiB parts
     assert big_part_rows(1 << 24, 512, 512) == 8192          # 8 GiB: capped at 4 MiB
     assert big_part_rows(1 << 21, 256, 1024) == 4096         # bf16 D=128, 512 MiB: 1 MiB parts
     assert big_part_rows(1_040_746, 512, 512) == 1024        # C2 (508 MiB): 2032 rows per 512th -> 1024
-    assert big_part_rows(655_360, 512, 512) == 1024          # f32 D=128, exactly 320 MiB
-    assert big_part_rows(655_359, 512, 512) == 512           # one row less: the default
-    assert big_part_rows(1 << 20, 304, 862) == 862           # the suites' largest (f32 D=76, 304 MiB)
+    assert big_part_rows(524_288, 512, 512) == 1024          # f32 D=128, exactly 256 MiB
+    assert big_part_rows(524_287, 512, 512) == 512           # one row less: the default
+    assert big_part_rows(1 << 20, 304, 862) == 1724          # the suites' largest (f32 D=76, 304 MiB)
+    assert big_part_rows(1 << 18, 512, 512) == 512           # 128 MiB: the default
     assert big_part_rows(1 << 27, 8, 32768) == 262144        # f32 D=2, 1 GiB: N/512 rows (2 MiB)
     assert big_block_rows(1 << 23, 8192, 1024) == 8192        # N/1024 = 8192 rows
     assert big_block_rows(1 << 22, 8192, 1024) == 4096        # N/1024 below the part
