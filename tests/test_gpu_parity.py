@@ -453,6 +453,10 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
     t_block = runtime.big_block_rows(int(offsets[-1]), rows, default_block)
     assert report.selection["t_block"] == report.thresholds[1] == t_block == 1415
     check(actual, values, offsets, op=op, dtype="f32")
+    # The same call with the offsets checked on the device first.
+    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified", mode="checked")
+    assert report.mode == "checked" and report.selection["part_rows"] == rows
+    check(actual, values, offsets, op=op, dtype="f32")
     shipped = runtime.big_block_rows
     monkeypatch.setattr(runtime, "big_block_rows", lambda n, part_rows, default_t_block: default_t_block)
     actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
