@@ -97,17 +97,21 @@ def _grid(ds, elements, segments, seed0, count, seed_grid):
 
 
 SUITES = ("train", "heldout", "heldout2", "heldout3", "train_dense", "heldout4", "heldout5", "heldout6",
-          "heldout7", "heldout8", "heldout9", "heldout10", "heldout11")
+          "heldout7", "heldout8", "heldout9", "heldout10", "heldout11", "heldout12")
 
 
 def suite(name: str) -> list[Case]:
     """The fixed shape suites. The held-out suites share no feature width,
     size or segment count with either train suite or with each other;
     heldout, heldout2, heldout3, heldout5, heldout6, heldout7, heldout8,
-    heldout9, heldout10 and heldout11 reach beyond the 256 MiB Infinity Cache
-    (working sets up to 512, 384, 320, 384, 576, 352, 416, 480, 544 and 608
-    MiB). Each was frozen before the fit it scores and scored once for it:
-    ``heldout11`` was defined, pinned and committed before any of it was
+    heldout9, heldout10, heldout11 and heldout12 reach beyond the 256 MiB
+    Infinity Cache (working sets up to 512, 384, 320, 384, 576, 352, 416, 480,
+    544, 608 and 672 MiB). Each was frozen before the fit it scores and scored
+    once for it: ``heldout12`` was defined, pinned and committed before any of
+    it was measured, to score version 7 refitted on the twelve training suites
+    measured with the runtime's larger split parts and block class for large
+    sum / max calls (its largest inputs, 336 MiB, take them); ``heldout11``
+    was defined, pinned and committed before any of it was
     measured, to score the boosted model form (version 7) fitted on every
     earlier suite measured on the build whose classification reserves split
     items in one round of atomics; ``heldout10`` was
@@ -168,6 +172,9 @@ def suite(name: str) -> list[Case]:
     if name == "heldout11":
         return _grid(ds=(23, 42, 76, 152, 232), elements=(19 << 18, 19 << 21, 19 << 22),
                      segments=(960, 3584, 61440), seed0=45000, count=150, seed_grid=89)
+    if name == "heldout12":
+        return _grid(ds=(25, 46, 84, 168, 216), elements=(21 << 18, 21 << 21, 21 << 22),
+                     segments=(1088, 2816, 69632), seed0=49000, count=150, seed_grid=97)
     raise ValueError(f"suite must be one of {SUITES}")
 
 

@@ -45,7 +45,7 @@ def test_suites_are_fixed_and_disjoint():
     assert {name: len(cases) for name, cases in suites.items()} == {
         "train": 330, "train_dense": 420, "heldout": 150, "heldout2": 150, "heldout3": 150, "heldout4": 150,
         "heldout5": 150, "heldout6": 150, "heldout7": 150, "heldout8": 150, "heldout9": 150, "heldout10": 150,
-        "heldout11": 150}
+        "heldout11": 150, "heldout12": 150}
     held = [name for name in suites if name.startswith("heldout")]
     pairs = [(a, b) for a in held for b in held if a < b] + [(t, h) for t in ("train", "train_dense") for h in held]
     for a, b in pairs:
@@ -56,7 +56,7 @@ def test_suites_are_fixed_and_disjoint():
     # Some working sets (rows read plus rows written) of most held-out suites
     # (the shipped model's heldout8 among them) exceed the 256 MiB Infinity Cache.
     for suite in (suites[name] for name in ("heldout", "heldout2", "heldout3", "heldout5", "heldout6", "heldout7",
-                                            "heldout8", "heldout9", "heldout10", "heldout11")):
+                                            "heldout8", "heldout9", "heldout10", "heldout11", "heldout12")):
         assert any(c.n * c.d * c.element_bytes * (2 if c.op == "softmax" else 1) > 256 << 20 for c in suite)
     # heldout2's shapes: fixed by its seed (a change of the suite would
     # silently unfreeze it).
@@ -67,6 +67,7 @@ def test_suites_are_fixed_and_disjoint():
     assert [c.key for c in suites["heldout9"][:3]] == FROZEN_HELDOUT9_HEAD
     assert [c.key for c in suites["heldout10"][:3]] == FROZEN_HELDOUT10_HEAD
     assert [c.key for c in suites["heldout11"][:3]] == FROZEN_HELDOUT11_HEAD
+    assert [c.key for c in suites["heldout12"][:3]] == FROZEN_HELDOUT12_HEAD
 
 
 FROZEN_HELDOUT2_HEAD = ["sum-f32-d3-n262144-b8192-long_tail-s9000", "sum-f32-d3-n262144-b8192-burst-s9001",
@@ -83,6 +84,8 @@ FROZEN_HELDOUT10_HEAD = ["sum-f32-d21-n1697694-b832-burst-s41000", "sum-f32-d21-
                          "sum-f32-d21-n3395388-b832-bimodal-s41002"]
 FROZEN_HELDOUT11_HEAD = ["sum-f32-d23-n216553-b61440-uniform-s45000", "sum-f32-d23-n216553-b61440-exponential-s45001",
                          "sum-f32-d23-n1732429-b960-burst-s45002"]
+FROZEN_HELDOUT12_HEAD = ["sum-f32-d25-n220200-b1088-bimodal-s49000", "sum-f32-d25-n220200-b1088-exponential-s49001",
+                         "sum-f32-d25-n220200-b69632-uniform-s49002"]
 
 
 @pytest.mark.parametrize("op", ["sum", "max", "softmax"])
