@@ -209,6 +209,28 @@ def test_shipped_model_records_its_heldout_scores():
     assert loso == model.calibration["leave_one_suite_out"]
 
 
+# The commit that froze heldout12's definition (and pinned its first keys)
+# before any of it was measured; the shipped model was scored on it once.
+HELDOUT12_COMMIT = "ec0b013"
+
+
+def test_shipped_model_records_its_heldout12_check():
+    """heldout12, defined and committed alone before any of it was measured
+    and measured with the library the model records, scores the shipped
+    model warm and cold exactly as recorded in its checks (at least 90%);
+    every measured case passed the sampled correctness gate."""
+    base = Path(calibrate.__file__).with_name("calibration")
+    records = calibrate.load(base / "heldout12.jsonl")
+    assert {r["key"] for r in records} == {c.key for c in calibrate.suite("heldout12")}
+    assert all(0.0 <= g <= 1.0 for r in records for g in r["gate"].values())
+    model = CostModel.load()
+    assert {r["library_sha256"] for r in records} == {model.calibration["library_sha256"]}
+    recorded = model.calibration["checks"]["heldout12.jsonl"]
+    warm, cold = calibrate.evaluate(model, records), calibrate.evaluate(model, records, cold=True)
+    assert recorded == {"cases": 150, "within_3pct": warm["share"], "within_3pct_cold": cold["share"]}
+    assert warm["share"] >= 0.9 and cold["share"] >= 0.9
+
+
 def test_transfer_onto_the_shipped_measurements_reproduces_the_shipped_model(tmp_path):
     """`transfer` (reference bench/calibrate.py:229-272) refits on another
     device's train measurements: run on the measurements the shipped model
