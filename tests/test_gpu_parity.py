@@ -426,11 +426,13 @@ def test_worker_deferred_split_parts_match(artifact_cache, d, dtype, masked):
     assert np.array_equal(actual, baseline, equal_nan=True)
 
 
+@pytest.mark.parametrize("dtype,offsets_dtype", [("f32", "i64"), ("bf16", "i32")])
 @pytest.mark.parametrize("op", ["sum", "max"])
-def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op):
+def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, op, dtype, offsets_dtype):
     """Sum / max calls of more than about 256 MiB of rows split long segments
     into parts of about N/512 rows and send segments of up to N/1024 rows to
-    the block class (a companion module): on a 742 MB call the result matches
+    the block class (a companion module): on a 742 MB (f32) or 371 MB (bf16,
+    i32 offsets) call the result matches
     the oracle (max bit-exact) and the report names the part size and block
     threshold. The same (N, B) on a module with another block threshold gets
     a plan of its own (plans are keyed by module). A call whose max_len fits
@@ -438,43 +440,45 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
     from ragged import runtime
     from ragged.workloads import offsets_from_lengths
     from gpu_helpers import check, run_program
-    program = Compiler().compile(ProgramSpec(op, "f32", 128, "i64"), artifact_cache)
+    program = Compiler().compile(ProgramSpec(op, dtype, 128, offsets_dtype), artifact_cache)
     default_rows = int(program.metadata["part_rows"])
     default_block = int(program.metadata["thresholds"][1])
-    # Around the default block threshold (1,024 rows), the raised one (1,415)
-    # and the part (2,048): block, one split part, two parts.
+    row_bytes = 128 * (2 if dtype == "bf16" else 4)
+    # f32: around the default block threshold (1,024 rows), the raised one
+    # (1,415) and the part (2,048): block, one split part, two parts. bf16:
+    # the default block threshold is the part (2,048 rows).
     lengths = np.array([(1 << 20) + (1 << 18), 1 << 17, 2049, 2048, 1500, 1025, default_block, 100, 0, 7],
                        dtype=np.int64)
-    offsets = offsets_from_lengths(lengths, "i64")
+    offsets = offsets_from_lengths(lengths, offsets_dtype)
     values = np.random.default_rng(5).normal(size=(int(offsets[-1]), 128)).astype(np.float32)
-    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
-    rows = runtime.big_part_rows(int(offsets[-1]), 512, default_rows)
+    actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified")
+    rows = runtime.big_part_rows(int(offsets[-1]), row_bytes, default_rows)
     assert report.selection.get("part_rows") == rows == 2048 > default_rows
     t_block = runtime.big_block_rows(int(offsets[-1]), rows, default_block)
-    assert report.selection["t_block"] == report.thresholds[1] == t_block == 1415
-    check(actual, values, offsets, op=op, dtype="f32")
+    assert report.selection["t_block"] == report.thresholds[1] == t_block == (1415 if dtype == "f32" else 2048)
+    check(actual, values, offsets, op=op, dtype=dtype)
     # The same call with the offsets checked on the device first.
-    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified", mode="checked")
+    actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified", mode="checked")
     assert report.mode == "checked" and report.selection["part_rows"] == rows
-    check(actual, values, offsets, op=op, dtype="f32")
+    check(actual, values, offsets, op=op, dtype=dtype)
     shipped = runtime.big_block_rows
     monkeypatch.setattr(runtime, "big_block_rows", lambda n, part_rows, default_t_block: default_t_block)
-    actual, report = run_program(program, values, offsets, dtype="f32", op=op, select="classified")
+    actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified")
     assert report.selection["t_block"] == report.thresholds[1] == default_block
     plans = {int(plan.t_block) for (module, n, b, schedule), plan in program._plans.items()
              if (n, b, schedule) == (int(offsets[-1]), len(lengths), f"parts{rows}")}
     assert plans == {default_block, t_block}
-    check(actual, values, offsets, op=op, dtype="f32")
+    check(actual, values, offsets, op=op, dtype=dtype)
     monkeypatch.setattr(runtime, "big_block_rows", shipped)
-    short = offsets_from_lengths(np.array([default_block] * 4 + [3], dtype=np.int64), "i64")
+    short = offsets_from_lengths(np.array([default_block] * 4 + [3], dtype=np.int64), offsets_dtype)
     few = values[:int(short[-1])]
-    actual, report = run_program(program, few, short, dtype="f32", op=op, select="classified",
+    actual, report = run_program(program, few, short, dtype=dtype, op=op, select="classified",
                                  max_len=default_block)
     assert "part_rows" not in report.selection and report.thresholds[1] == default_block
-    check(actual, few, short, op=op, dtype="f32")
+    check(actual, few, short, op=op, dtype=dtype)
     # A small call that provably splits a segment: N/512 is below twice the
     # default part.
-    small = offsets_from_lengths(np.array([3000, 3], dtype=np.int64), "i64")
-    actual, report = run_program(program, values[:3003], small, dtype="f32", op=op, select="classified")
+    small = offsets_from_lengths(np.array([3 * default_block, 3], dtype=np.int64), offsets_dtype)
+    actual, report = run_program(program, values[:int(small[-1])], small, dtype=dtype, op=op, select="classified")
     assert "part_rows" not in report.selection
-    check(actual, values[:3003], small, op=op, dtype="f32")
+    check(actual, values[:int(small[-1])], small, op=op, dtype=dtype)
