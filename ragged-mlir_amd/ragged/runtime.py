@@ -93,11 +93,12 @@ def deferred_rows_bound(n: int, b: int, max_len: int | None, limit: int) -> int:
 # segments 546 -> 233; on the calibration suites' 32 training cases it
 # changes, 11% less time warm. Only calls that provably hold a segment longer
 # than the block class take them (``splits_segments``), and segments of up to
-# N/1024 rows join the block class (``big_block_rows``). The cost model was
+# about N/1024 rows join the block class (``big_block_rows``). The cost model was
 # fitted on measurements taken with these rules.
 BIG_PART_SHARE = 512
 BIG_PART_BYTES = 4 << 20
 BIG_BLOCK_SHARE = 1024
+BIG_BLOCK_STEPS = 8
 
 
 def big_part_rows(n: int, row_bytes: int, default_rows: int) -> int:
@@ -117,8 +118,11 @@ def big_block_rows(n: int, part_rows: int, default_t_block: int) -> int:
     whole, with no partial to publish (as one split part it costs 1.2-1.3x
     the time), up to n / BIG_BLOCK_SHARE rows (about 1.5 resident
     workgroups' share of the call: block items are taken after the split
-    parts, and larger ones finish last)."""
-    return max(default_t_block, min(part_rows, n // BIG_BLOCK_SHARE))
+    parts, and larger ones finish last), rounded down to a multiple of
+    part_rows / BIG_BLOCK_STEPS, so that a program keeps at most that many
+    companion modules per part size."""
+    step = max(1, part_rows // BIG_BLOCK_STEPS)
+    return max(default_t_block, min(part_rows, n // BIG_BLOCK_SHARE // step * step))
 
 
 def splits_segments(n: int, b: int, max_len: int | None, t_block: int) -> bool:

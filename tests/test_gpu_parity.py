@@ -445,7 +445,7 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
     default_block = int(program.metadata["thresholds"][1])
     row_bytes = 128 * (2 if dtype == "bf16" else 4)
     # f32: around the default block threshold (1,024 rows), the raised one
-    # (1,415) and the part (2,048): block, one split part, two parts. bf16:
+    # (1,280) and the part (2,048): block, one split part, two parts. bf16:
     # the default block threshold is the part (2,048 rows).
     lengths = np.array([(1 << 20) + (1 << 18), 1 << 17, 2049, 2048, 1500, 1025, default_block, 100, 0, 7],
                        dtype=np.int64)
@@ -455,7 +455,7 @@ def test_big_reduce_calls_take_larger_split_parts(artifact_cache, monkeypatch, o
     rows = runtime.big_part_rows(int(offsets[-1]), row_bytes, default_rows)
     assert report.selection.get("part_rows") == rows == 2048 > default_rows
     t_block = runtime.big_block_rows(int(offsets[-1]), rows, default_block)
-    assert report.selection["t_block"] == report.thresholds[1] == t_block == (1415 if dtype == "f32" else 2048)
+    assert report.selection["t_block"] == report.thresholds[1] == t_block == (1280 if dtype == "f32" else 2048)
     check(actual, values, offsets, op=op, dtype=dtype)
     # The same call with the offsets checked on the device first.
     actual, report = run_program(program, values, offsets, dtype=dtype, op=op, select="classified", mode="checked")

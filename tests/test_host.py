@@ -265,7 +265,7 @@ def test_big_part_rows_known_answers():
     """Sum / max calls split into parts of about N/512 rows, at most 4 MiB,
     at least the library's default, which they keep while N/512 is below
     twice it (about 256 MiB of rows). Segments of up to N/1024 rows (at most
-    a part) go to the block class."""
+    a part, rounded down to an eighth of it) go to the block class."""
     from ragged.runtime import big_block_rows, big_part_rows
     assert big_part_rows(1 << 22, 512, 512) == 8192          # f32 D=128, 2 GiB: 4 MiB parts
     assert big_part_rows(1 << 22, 256, 1024) == 8192         # bf16 D=128, 1 GiB: 2 MiB parts
@@ -281,7 +281,10 @@ def test_big_part_rows_known_answers():
     assert big_block_rows(1 << 22, 8192, 1024) == 4096        # N/1024 below the part
     assert big_block_rows(1 << 24, 8192, 1024) == 8192        # at most the part
     assert big_block_rows(1 << 20, 2048, 1024) == 1024        # at least the default
-    assert big_block_rows(1_449_545, 2048, 1024) == 1415
+    assert big_block_rows(1_449_545, 2048, 1024) == 1280       # 1,415 rounded down to an eighth of the part
+    assert big_block_rows(8_003_578, 8192, 1024) == 7168       # 7,815 -> 7 x 1,024
+    # At most BIG_BLOCK_STEPS distinct thresholds (companion modules) per part size.
+    assert len({big_block_rows(n, 8192, 1024) for n in range(1 << 22, 1 << 24, 99_991)}) <= 8
 
 
 def test_splits_segments_known_answers():
